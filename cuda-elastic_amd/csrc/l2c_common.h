@@ -1,0 +1,75 @@
+// Device-side helpers shared by the l2c kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cfloat>
+#include <cstdint>
+
+#define L2C_WAVE 64
+
+namespace l2c {
+
+// Butterfly sum over the 64 lanes of a wavefront; every lane gets the total.
+// __shfl_xor lowers to ds_swizzle / ds_bpermute, which use the LDS crossbar
+// but no LDS allocation.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, L2C_WAVE);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, L2C_WAVE));
+  return v;
+}
+
+// Block-wide reductions through one LDS slot per wave. Every thread returns
+// the result. Each call site passes its own slot array, so two reductions in
+// a row need no barrier between them. The cross-wave sum runs in wave order,
+// so the result does not depend on scheduling.
+__device__ __forceinline__ float block_sum(float v, float *slots) {
+  v = wave_sum(v);
+  const int waves = blockDim.x / L2C_WAVE;
+  if (threadIdx.x % L2C_WAVE == 0) slots[threadIdx.x / L2C_WAVE] = v;
+  __syncthreads();
+  float total = 0.0f;
+  for (int w = 0; w < waves; ++w) total += slots[w];
+  return total;
+}
+
+__device__ __forceinline__ float block_max(float v, float *slots) {
+  v = wave_max(v);
+  const int waves = blockDim.x / L2C_WAVE;
+  if (threadIdx.x % L2C_WAVE == 0) slots[threadIdx.x / L2C_WAVE] = v;
+  __syncthreads();
+  float m = -FLT_MAX;
+  for (int w = 0; w < waves; ++w) m = fmaxf(m, slots[w]);
+  return m;
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte loads and stores with the nontemporal hint: data touched once
+// streams through the caches without displacing reused operands.
+__device__ __forceinline__ float4 ld4_stream(const float4 *p) {
+  const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void st4_stream(float4 *p, float4 v) {
+  const f32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<f32x4 *>(p));
+}
+
+}  // namespace l2c
+
+// Return code plumbing shared by the extern "C" entry points.
+#define L2C_LAUNCH_CHECK()                      \
+  do {                                          \
+    hipError_t e__ = hipGetLastError();         \
+    if (e__ != hipSuccess) return (int)e__;     \
+  } while (0)
+
+static inline bool l2c_aligned16(const void *p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}

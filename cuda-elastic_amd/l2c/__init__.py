@@ -1,0 +1,254 @@
+"""Python binding of the llama2c hot path on MI355X.
+
+Loads the in-tree libl2c.so (HIP kernels behind the C ABI of include/l2c.h)
+and libl2c_host.so (the harness, include/l2c_harness.h) with ctypes. Device
+memory and streams come from torch: every wrapper takes torch tensors on the
+GPU and enqueues on torch's current stream (or the stream passed in).
+
+There is no fallback: if the built library is missing or a call fails, an
+exception is raised.
+
+The wrappers mirror the reference kernels' argument order and meaning
+(llama2c/llama2c_cuda_graph.cu:58-162, llama2c_sota.cu:263-298).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import shlex
+import subprocess
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+BIN_DIR = os.path.join(PKG_DIR, "bin")
+LIB_PATH = os.path.join(LIB_DIR, "libl2c.so")
+HOST_LIB_PATH = os.path.join(LIB_DIR, "libl2c_host.so")
+HARNESS = os.path.join(BIN_DIR, "llama2c_hip")
+COMPARE = os.path.join(BIN_DIR, "l2c_compare")
+
+RMS_EPSILON = 1.0e-5  # llama2c/llama2c_common.h:44
+
+MATVEC_NAIVE = 0
+MATVEC_COALESCED = 1
+Q_MXFP4 = 0
+Q_FP8 = 1
+OP_RMSNORM, OP_SOFTMAX, OP_MATVEC, OP_FUSED, OP_MATMUL, OP_MATMUL_Q = range(6)
+
+# Symbols declared in include/l2c.h and include/l2c_harness.h.
+KERNEL_SYMBOLS = (
+    "l2c_rmsnorm", "l2c_softmax", "l2c_matvec", "l2c_fused", "l2c_matmul", "l2c_matmul_q",
+    "l2c_quantize_mxfp4", "l2c_quantize_fp8", "l2c_to_bf16", "l2c_launch_shape",
+    "l2c_strerror", "l2c_version",
+)
+HOST_SYMBOLS = ("l2c_harness_main", "l2c_compare_dumps")
+
+
+class L2CError(RuntimeError):
+    """A nonzero return code from the C ABI."""
+
+
+def build(jobs: int = 8) -> None:
+    """Compiles the package (make -C cuda-elastic_amd)."""
+    subprocess.run(["make", "-C", PKG_DIR, f"-j{jobs}"], check=True)
+
+
+_lib = None
+_host = None
+
+
+def _vp(x):
+    return ctypes.c_void_p(x)
+
+
+def load() -> ctypes.CDLL:
+    """Loads libl2c.so (after torch, so both share one HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FileNotFoundError(
+            f"{LIB_PATH} is not built; run `make -C {PKG_DIR}` (or __graft_entry__.build())")
+    try:
+        import torch  # noqa: F401  (loads the HIP runtime torch was built with first)
+    except ImportError:
+        pass
+    lib = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+    i, f, p, sz = ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+    sigs = {
+        "l2c_rmsnorm": [p, p, p, i, i, f, p],
+        "l2c_softmax": [p, p, i, i, p],
+        "l2c_matvec": [p, p, p, i, i, i, p],
+        "l2c_fused": [p, p, p, p, p, p, p, i, i, i, i, f, p],
+        "l2c_matmul": [p, p, p, i, i, i, p],
+        "l2c_matmul_q": [p, p, p, p, i, i, i, i, p],
+        "l2c_quantize_mxfp4": [p, p, p, i, i, p],
+        "l2c_quantize_fp8": [p, p, p, i, i, p],
+        "l2c_to_bf16": [p, p, sz, p],
+        "l2c_launch_shape": [i, i, i, i, i, ctypes.POINTER(i), ctypes.POINTER(i), ctypes.POINTER(i)],
+    }
+    for name, args in sigs.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int
+    lib.l2c_strerror.argtypes = [ctypes.c_int]
+    lib.l2c_strerror.restype = ctypes.c_char_p
+    lib.l2c_version.argtypes = []
+    lib.l2c_version.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def load_host() -> ctypes.CDLL:
+    """Loads libl2c_host.so (the harness library)."""
+    global _host
+    if _host is not None:
+        return _host
+    load()
+    if not os.path.exists(HOST_LIB_PATH):
+        raise FileNotFoundError(f"{HOST_LIB_PATH} is not built")
+    host = ctypes.CDLL(HOST_LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+    host.l2c_harness_main.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
+                                      ctypes.c_char_p, ctypes.c_size_t]
+    host.l2c_harness_main.restype = ctypes.c_int
+    host.l2c_compare_dumps.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_char_p)]
+    host.l2c_compare_dumps.restype = ctypes.c_int
+    _host = host
+    return host
+
+
+def _check(code: int, what: str) -> None:
+    if code != 0:
+        msg = load().l2c_strerror(code).decode()
+        raise L2CError(f"{what} failed: {msg} ({code})")
+
+
+def _stream(stream):
+    if stream is not None:
+        return stream if isinstance(stream, int) else stream.cuda_stream
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("l2c wrappers take GPU tensors")
+    return t.data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# Kernel wrappers (torch tensors in, results in `out`).
+
+def rmsnorm(out, inp, weight, size, batch, eps=RMS_EPSILON, stream=None):
+    _check(load().l2c_rmsnorm(_vp(_ptr(out)), _vp(_ptr(inp)), _vp(_ptr(weight)), size, batch,
+                              eps, _vp(_stream(stream))), "l2c_rmsnorm")
+
+
+def softmax(out, logits, size, batch, stream=None):
+    _check(load().l2c_softmax(_vp(_ptr(out)), _vp(_ptr(logits)), size, batch,
+                              _vp(_stream(stream))), "l2c_softmax")
+
+
+def matvec(out, x, W, cols, rows, variant=MATVEC_COALESCED, stream=None):
+    _check(load().l2c_matvec(_vp(_ptr(out)), _vp(_ptr(x)), _vp(_ptr(W)), cols, rows, variant,
+                             _vp(_stream(stream))), "l2c_matvec")
+
+
+def fused(normalized, inp, weight, softmax_out, logits, product, matrix, size, rms_rows,
+          softmax_rows, matmul_rows, eps=RMS_EPSILON, stream=None):
+    _check(load().l2c_fused(_vp(_ptr(normalized)), _vp(_ptr(inp)), _vp(_ptr(weight)),
+                            _vp(_ptr(softmax_out)), _vp(_ptr(logits)), _vp(_ptr(product)),
+                            _vp(_ptr(matrix)), size, rms_rows, softmax_rows, matmul_rows, eps,
+                            _vp(_stream(stream))), "l2c_fused")
+
+
+def matmul(out, X, W, batch, cols, rows, stream=None):
+    _check(load().l2c_matmul(_vp(_ptr(out)), _vp(_ptr(X)), _vp(_ptr(W)), batch, cols, rows,
+                             _vp(_stream(stream))), "l2c_matmul")
+
+
+def matmul_q(out, xbf16, wq, scales, fmt, batch, cols, rows, stream=None):
+    _check(load().l2c_matmul_q(_vp(_ptr(out)), _vp(_ptr(xbf16)), _vp(_ptr(wq)), _vp(_ptr(scales)),
+                               fmt, batch, cols, rows, _vp(_stream(stream))), "l2c_matmul_q")
+
+
+def quantize_mxfp4(codes, scales, W, rows, cols, stream=None):
+    _check(load().l2c_quantize_mxfp4(_vp(_ptr(codes)), _vp(_ptr(scales)), _vp(_ptr(W)), rows, cols,
+                                     _vp(_stream(stream))), "l2c_quantize_mxfp4")
+
+
+def quantize_fp8(codes, scales, W, rows, cols, stream=None):
+    _check(load().l2c_quantize_fp8(_vp(_ptr(codes)), _vp(_ptr(scales)), _vp(_ptr(W)), rows, cols,
+                                   _vp(_stream(stream))), "l2c_quantize_fp8")
+
+
+def to_bf16(out, inp, n, stream=None):
+    _check(load().l2c_to_bf16(_vp(_ptr(out)), _vp(_ptr(inp)), n, _vp(_stream(stream))),
+           "l2c_to_bf16")
+
+
+def launch_shape(op, batch, cols, rows, variant=0):
+    g, b, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _check(load().l2c_launch_shape(op, batch, cols, rows, variant, ctypes.byref(g),
+                                   ctypes.byref(b), ctypes.byref(c)), "l2c_launch_shape")
+    return g.value, b.value, c.value
+
+
+# ---------------------------------------------------------------------------
+# Harness
+
+def parse_line(line: str) -> dict:
+    """Parses the key=value result line into a dict (numbers converted)."""
+    out = {}
+    for token in line.split():
+        if "=" not in token:
+            continue
+        k, v = token.split("=", 1)
+        try:
+            out[k] = int(v)
+        except ValueError:
+            try:
+                out[k] = float(v)
+            except ValueError:
+                out[k] = v
+    return out
+
+
+def harness(args, in_process: bool = True, env=None, timeout=None):
+    """Runs one harness invocation; returns (exit_code, parsed line, raw line).
+
+    args is the argument list after the program name, e.g.
+    ["graph", "3", "1024", "16384", "8192", "1", "1", "nocopy", "batched", "scaled"].
+    """
+    args = [str(a) for a in args]
+    if in_process:
+        host = load_host()
+        argv = [b"llama2c_hip"] + [a.encode() for a in args]
+        arr = (ctypes.c_char_p * len(argv))(*argv)
+        buf = ctypes.create_string_buffer(8192)
+        code = host.l2c_harness_main(len(argv), arr, buf, len(buf))
+        line = buf.value.decode()
+        return code, parse_line(line), line
+    if not os.path.exists(HARNESS):
+        raise FileNotFoundError(f"{HARNESS} is not built")
+    proc = subprocess.run([HARNESS] + args, capture_output=True, text=True, env=env,
+                          timeout=timeout)
+    line = proc.stdout.strip().splitlines()[-1] if proc.stdout.strip() else ""
+    if proc.returncode != 0 and proc.stderr:
+        line = line or ""
+    return proc.returncode, parse_line(line), line + ("\n" + proc.stderr if proc.stderr else "")
+
+
+def compare_dumps(paths, in_process: bool = False):
+    """Runs the dump comparer; returns (exit_code, report text)."""
+    if in_process:
+        host = load_host()
+        arr = (ctypes.c_char_p * len(paths))(*[p.encode() for p in paths])
+        return host.l2c_compare_dumps(len(paths), arr), ""
+    proc = subprocess.run([COMPARE] + list(paths), capture_output=True, text=True)
+    return proc.returncode, proc.stdout + proc.stderr
+
+
+def command_line(args) -> str:
+    return " ".join(shlex.quote(a) for a in [HARNESS] + [str(a) for a in args])

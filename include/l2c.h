@@ -1,0 +1,159 @@
+/*
+ * l2c.h -- C ABI of the MI355X (gfx950) llama2c hot path: rmsnorm, softmax and
+ * the W.x matmul, as hand-written HIP kernels in libl2c.so.
+ *
+ * Every entry point only enqueues work on `stream`. It does not allocate,
+ * synchronize or read device data on the host, so every call may be recorded
+ * into a hipGraph with hipStreamBeginCapture. All pointers are caller-owned
+ * device memory. float pointers must be 4-byte aligned; the kernels take
+ * 16-byte vector paths when a row's address allows it and scalar paths
+ * otherwise, so any alignment the HIP allocator hands out plus any row
+ * offset is accepted.
+ *
+ * Return value: 0 (hipSuccess) or a hipError_t value. Bad arguments give
+ * hipErrorInvalidValue (1) and enqueue nothing; a failed launch returns the
+ * error reported by hipGetLastError after the launch, as the reference checks
+ * cudaGetLastError after each launch (llama2c/llama2c_cuda_graph.cu:357,360,367).
+ * l2c_strerror() names any returned code.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   l2c_rmsnorm   rmsnorm_kernel        llama2c/llama2c_cuda_graph.cu:58-78 (launch :355-357)
+ *   l2c_softmax   softmax_kernel        llama2c/llama2c_cuda_graph.cu:82-115 (launch :358-360)
+ *   l2c_matvec    matmul_kernel / matmul_coalesced_kernel
+ *                                       llama2c/llama2c_cuda_graph.cu:119-162 (launch :361-367)
+ *   l2c_fused     llama2c_sota_kernel   llama2c/llama2c_sota.cu:79-298 (launch :451-455)
+ *   l2c_matmul    classifier_kernel     applications/loom_private/decoder/decoder.cu:79-125
+ *   l2c_matmul_q  no kernel in the reference: the quantized-weight matmul of the
+ *                 benchmark configuration (MXFP4 / per-row fp8 weights, bf16
+ *                 activations); its codes follow experiments/blackwell/lowprec/reference.cpp:13-96
+ */
+#ifndef L2C_H
+#define L2C_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Matrix-vector variants of l2c_matvec (the reference's `naive|coalesced` token). */
+enum l2c_matvec_variant {
+  L2C_MATVEC_NAIVE = 0,     /* one lane per output row (llama2c_cuda_graph.cu:119-128) */
+  L2C_MATVEC_COALESCED = 1  /* rows streamed by whole wavefronts (llama2c_cuda_graph.cu:134-162) */
+};
+
+/* Weight formats of l2c_matmul_q. */
+enum l2c_qformat {
+  L2C_Q_MXFP4 = 0, /* e2m1 codes, two per byte (even k in the low nibble), one e8m0
+                      scale byte per 32 consecutive k of a row: scales[r][k/32] */
+  L2C_Q_FP8 = 1    /* e4m3 (OCP, bias 7, 0x7f/0xff NaN) codes, one byte each, and one
+                      fp32 scale per row: scales[r] */
+};
+
+/*
+ * out[b][j] = in[b][j] * (1 / sqrt(sum_j in[b][j]^2 / size + eps)) * weight[j]
+ * for b < batch, j < size; rows are `size` floats apart.
+ * Replaces rmsnorm_kernel, llama2c/llama2c_cuda_graph.cu:58-78.
+ */
+int l2c_rmsnorm(float *out, const float *in, const float *weight, int size, int batch,
+                float eps, hipStream_t stream);
+
+/*
+ * out[b][j] = exp(logits[b][j] - max_b) / sum_j exp(logits[b][j] - max_b).
+ * out may equal logits (in place).
+ * Replaces softmax_kernel, llama2c/llama2c_cuda_graph.cu:82-115.
+ */
+int l2c_softmax(float *out, const float *logits, int size, int batch, hipStream_t stream);
+
+/*
+ * out[r] = sum_{c < cols} W[r][c] * x[c] for r < rows (W row-major, rows x cols).
+ * variant: enum l2c_matvec_variant.
+ * Replaces matmul_kernel / matmul_coalesced_kernel, llama2c/llama2c_cuda_graph.cu:119-162.
+ */
+int l2c_matvec(float *out, const float *x, const float *W, int cols, int rows, int variant,
+               hipStream_t stream);
+
+/*
+ * All three operations of one llama2c iteration in one launch:
+ *   normalized = rmsnorm(input, weight) over rms_rows rows,
+ *   softmax    = softmax(logits) over softmax_rows rows,
+ *   product    = matrix . input[0:size] over matmul_rows rows.
+ * Any of the three row counts may be 0. Replaces llama2c_sota_kernel,
+ * llama2c/llama2c_sota.cu:79-298 (its Work struct, :79-94).
+ */
+int l2c_fused(float *normalized, const float *input, const float *weight, float *softmax,
+              const float *logits, float *product, const float *matrix, int size,
+              int rms_rows, int softmax_rows, int matmul_rows, float eps, hipStream_t stream);
+
+/*
+ * Batched fp32 contraction on the fp32 matrix cores:
+ *   out[b][r] = sum_{k < cols} W[r][k] * X[b][k], b < batch, r < rows
+ * X is batch x cols, W is rows x cols, out is batch x rows, all row-major.
+ * Same contraction as classifier_kernel,
+ * applications/loom_private/decoder/decoder.cu:79-125 (logits = cls . norm).
+ */
+int l2c_matmul(float *out, const float *X, const float *W, int batch, int cols, int rows,
+               hipStream_t stream);
+
+/*
+ * Quantized-weight contraction:
+ *   out[b][r] = sum_k Xbf16[b][k] * dequant(Wq, scales)[r][k]
+ * Xbf16: batch x cols bfloat16 (uint16 bit patterns); fmt: enum l2c_qformat.
+ * L2C_Q_MXFP4 needs cols % 32 == 0; L2C_Q_FP8 any cols.
+ * No counterpart kernel in the reference (see the file header).
+ */
+int l2c_matmul_q(float *out, const void *Xbf16, const void *Wq, const void *scales, int fmt,
+                 int batch, int cols, int rows, hipStream_t stream);
+
+/*
+ * Quantizers for l2c_matmul_q's weight operand, run on the device (setup work,
+ * outside any timed region):
+ *   l2c_quantize_mxfp4: codes[r][k/2] (cols/2 bytes per row), scales[r][k/32];
+ *     block scale exponent X = floor(log2(amax / 6)) clamped to [-127, 127]
+ *     (amax = 0 gives X = -127 and zero codes); code = e2m1(w * 2^-X), nearest,
+ *     ties to the even code, saturating at 6, -0 encoded as +0.
+ *   l2c_quantize_fp8: codes[r][k], scales[r] = amax_r / 448 (1 if amax_r = 0);
+ *     code = e4m3(w / scales[r]), nearest-even, saturating at 448.
+ *   l2c_to_bf16: bf16 round-to-nearest-even of n floats.
+ */
+int l2c_quantize_mxfp4(uint8_t *codes, uint8_t *scales, const float *W, int rows, int cols,
+                       hipStream_t stream);
+int l2c_quantize_fp8(uint8_t *codes, float *scales, const float *W, int rows, int cols,
+                     hipStream_t stream);
+int l2c_to_bf16(uint16_t *out, const float *in, size_t n, hipStream_t stream);
+
+/* Operations named by l2c_launch_shape. */
+enum l2c_op {
+  L2C_OP_RMSNORM = 0,
+  L2C_OP_SOFTMAX = 1,
+  L2C_OP_MATVEC = 2,
+  L2C_OP_FUSED = 3,
+  L2C_OP_MATMUL = 4,
+  L2C_OP_MATMUL_Q = 5
+};
+
+/*
+ * Launch shape the library uses for one call of `op` (batch vectors of `cols`
+ * floats; `rows` matrix rows; variant = matvec variant or quantized format),
+ * and how many of its workgroups fit on one CU at once, for the harness's
+ * waves = grid / (blocks_per_cu * CUs) figures. The reference computes them
+ * inline with cudaOccupancyMaxActiveBlocksPerMultiprocessor,
+ * llama2c/llama2c_cuda_graph.cu:318-336. For L2C_OP_FUSED, batch is both the
+ * rmsnorm and softmax row count.
+ */
+int l2c_launch_shape(int op, int batch, int cols, int rows, int variant, int *grid, int *block,
+                     int *blocks_per_cu);
+
+/* Name of a code returned by any l2c_* call. */
+const char *l2c_strerror(int code);
+
+/* Library version string; also proves the library loaded. */
+const char *l2c_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* L2C_H */

@@ -1,0 +1,505 @@
+/*
+ * l2c_oracle.c -- CPU restatement of the reference's llama2c algorithm.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the checker: only tests/, the smoke
+ * check of __graft_entry__.py and the cpu_baseline leg of bench.py load it
+ * (as oracle/liboracle.so). The product (cuda-elastic_amd/) never links or
+ * calls it; the HIP kernels are the only thing measured or shipped.
+ *
+ * Every function cites the reference lines it follows (paths relative to the
+ * reference repository). How each one is pinned:
+ *   orc_uniform, orc_fill         : against oracle/_ref (the reference header
+ *                                   compiled as is) and committed fixtures
+ *   orc_normal                    : against oracle/_ref (lowprec make_fixture)
+ *   orc_gamma                     : against oracle/_ref and a closed form
+ *   orc_check_vectors,
+ *   orc_product_check             : against oracle/_ref validate_all on planted
+ *                                   errors, deterministic closed forms
+ *   orc_e2m1_encode, orc_ue4m3_encode, orc_bf16 : against oracle/_ref
+ *                                   (lowprec encode / to_bf16), exhaustively
+ *   orc_mxfp4_exponent            : closed form 6 * 2^X <= amax < 6 * 2^(X+1)
+ *   orc_iteration_f32             : llama2.c loop order; pinned against the
+ *                                   double references within fp32 bounds
+ *   orc_matvec_fma                : bit-exact sequential fmaf chain; pinned by
+ *                                   the deterministic closed form and the
+ *                                   double reference
+ * Build: oracle/Makefile (gcc, -O2, no fast-math, -ffp-contract=off).
+ */
+#include <float.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* Generators: llama2c/llama2c_common.h:90-132                               */
+
+uint64_t orc_splitmix64(uint64_t x) {
+  x += 0x9e3779b97f4a7c15ull;
+  x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+  x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+  return x ^ (x >> 31);
+}
+
+/* llama2c/llama2c_common.h:100-103 */
+float orc_uniform(uint64_t seed, uint64_t stream, uint64_t index) {
+  uint64_t bits = orc_splitmix64(orc_splitmix64(seed * 4 + stream) ^ index);
+  return (float)(int64_t)(bits >> 40) * (1.0f / 8388608.0f) - 1.0f;
+}
+
+/* experiments/blackwell/lowprec/spec.json:49 and reference.cpp:170-193:
+ * sequential splitmix64 seeded with seed * 0x100000001b3 + stream, uniform
+ * (x >> 11) 2^-53, Box-Muller over consecutive pairs. Restated here as a
+ * plain sequential generator walked to the requested pair. */
+float orc_normal(uint64_t seed, uint64_t stream, uint64_t index) {
+  uint64_t state = seed * 0x100000001b3ull + stream;
+  uint64_t pair = index / 2, d1, d2;
+  /* state after 2 * pair draws */
+  state += 2 * pair * 0x9e3779b97f4a7c15ull;
+  state += 0x9e3779b97f4a7c15ull;
+  d1 = state;
+  d1 = (d1 ^ (d1 >> 30)) * 0xbf58476d1ce4e5b9ull;
+  d1 = (d1 ^ (d1 >> 27)) * 0x94d049bb133111ebull;
+  d1 = d1 ^ (d1 >> 31);
+  state += 0x9e3779b97f4a7c15ull;
+  d2 = state;
+  d2 = (d2 ^ (d2 >> 30)) * 0xbf58476d1ce4e5b9ull;
+  d2 = (d2 ^ (d2 >> 27)) * 0x94d049bb133111ebull;
+  d2 = d2 ^ (d2 >> 31);
+  {
+    const double u1 = (double)(d1 >> 11) * 0x1.0p-53, u2 = (double)(d2 >> 11) * 0x1.0p-53;
+    const double radius = sqrt(-2.0 * log(1.0 - u1));
+    const double angle = 6.283185307179586476925286766559 * u2;
+    return (float)((index % 2 == 0) ? radius * cos(angle) : radius * sin(angle));
+  }
+}
+
+/* Input modes: 0 deterministic, 1 random (llama2c_common.h:105-132);
+ * 2 scaled and 3 normal (the benchmark-configuration distributions:
+ * weight = 1 + u/2, matrix = u / sqrt(size) or N(0,1) / sqrt(size)). */
+void orc_fill(int mode, uint64_t seed, int batch, int size, int rows, float *input,
+              float *probabilities, float *weight, float *matrix) {
+  const size_t n = (size_t)batch * size, m = (size_t)rows * size;
+  size_t i;
+  for (i = 0; i < (size_t)size; ++i) weight[i] = 1.0f;
+  memset(matrix, 0, m * sizeof(float));
+  if (mode == 0) {
+    int r;
+    for (i = 0; i < n; ++i) {
+      input[i] = 1.0f + (float)(i % 4);
+      probabilities[i] = 1.0f + (float)(i % 4);
+    }
+    for (r = 0; r < rows; ++r) matrix[(size_t)r * size + (size_t)(r % size)] = 1.0f;
+    return;
+  }
+  for (i = 0; i < n; ++i) {
+    input[i] = orc_uniform(seed, 0, i);
+    probabilities[i] = orc_uniform(seed, 1, i);
+  }
+  if (mode == 1) {
+    for (i = 0; i < (size_t)size; ++i) weight[i] = orc_uniform(seed, 2, i);
+    for (i = 0; i < m; ++i) matrix[i] = orc_uniform(seed, 3, i);
+    return;
+  }
+  for (i = 0; i < (size_t)size; ++i) weight[i] = 1.0f + 0.5f * orc_uniform(seed, 2, i);
+  {
+    const float inv_sqrt = (float)(1.0 / sqrt((double)size));
+    for (i = 0; i < m; ++i)
+      matrix[i] = (mode == 2 ? orc_uniform(seed, 3, i) : orc_normal(seed, 3, i)) * inv_sqrt;
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Validation rules: llama2c/llama2c_common.h:139-319                        */
+
+/* llama2c_common.h:231-235 */
+double orc_gamma(int n) {
+  const double u = ldexp(1.0, -24), lambda = 9.0;
+  return expm1(lambda * sqrt((double)n) * u + n * u * u / (1.0 - u));
+}
+
+/* Double references of rmsnorm and softmax for every vector
+ * (llama2c_common.h:243-262). */
+void orc_rmsnorm_ref(const float *x, const float *weight, int batch, int size, float eps,
+                     double *out) {
+  int b, j;
+  for (b = 0; b < batch; ++b) {
+    const float *v = x + (size_t)b * size;
+    double ss = 0.0, scale;
+    for (j = 0; j < size; ++j) ss += (double)v[j] * v[j];
+    scale = 1.0 / sqrt(ss / size + (double)eps);
+    for (j = 0; j < size; ++j) out[(size_t)b * size + j] = v[j] * scale * weight[j];
+  }
+}
+
+void orc_softmax_ref(const float *p, int batch, int size, double *out) {
+  int b, j;
+  for (b = 0; b < batch; ++b) {
+    const float *v = p + (size_t)b * size;
+    double mx = -DBL_MAX, sum = 0.0;
+    for (j = 0; j < size; ++j) mx = fmax(mx, (double)v[j]);
+    for (j = 0; j < size; ++j) sum += exp(v[j] - mx);
+    for (j = 0; j < size; ++j) out[(size_t)b * size + j] = exp(v[j] - mx) / sum;
+  }
+}
+
+/*
+ * Checks normalized and softmax for every vector with the rules of
+ * llama2c_common.h:237-276 (and, for deterministic inputs, :150-190 in float
+ * arithmetic). Returns 1 when valid. err[0..3] receive the largest rmsnorm
+ * absolute and relative errors and softmax absolute and relative errors.
+ */
+int orc_check_vectors(int deterministic, const float *input, const float *probabilities,
+                      const float *weight, const float *normalized, const float *softmax,
+                      int batch, int size, double *err) {
+  int valid = 1, b, j;
+  const float eps = 1.0e-5f;
+  double e0 = 0, e1 = 0, e2 = 0, e3 = 0;
+  for (b = 0; b < batch; ++b) {
+    const size_t off = (size_t)b * size;
+    const float *x = input + off, *p = probabilities + off;
+    double ss = 0.0, scale, mx = -DBL_MAX, es = 0.0, psum = 0.0;
+    for (j = 0; j < size; ++j) ss += (double)x[j] * x[j];
+    scale = 1.0 / sqrt(ss / size + (double)eps);
+    for (j = 0; j < size; ++j) mx = fmax(mx, (double)p[j]);
+    for (j = 0; j < size; ++j) es += exp(p[j] - mx);
+    for (j = 0; j < size; ++j) {
+      const double expected = x[j] * scale * weight[j];
+      const double got = normalized[off + j];
+      const double d = fabs(got - expected);
+      const double ep = exp(p[j] - mx) / es;
+      const double actual = softmax[off + j];
+      const double ds = fabs(actual - ep);
+      if (!(d <= 3.0e-4)) valid = 0;
+      if (!(ds <= 1.0e-9 + 1.0e-3 * ep)) valid = 0;
+      if (!isfinite(actual) || actual < 0.0) valid = 0;
+      if (d != d) {
+        e0 = e1 = INFINITY;
+      } else {
+        if (d > e0) e0 = d;
+        if (expected != 0.0 && d / fabs(expected) > e1) e1 = d / fabs(expected);
+      }
+      if (ds != ds) {
+        e2 = e3 = INFINITY;
+      } else {
+        if (ds > e2) e2 = ds;
+        if (ep > 0.0 && ds / ep > e3) e3 = ds / ep;
+      }
+      psum += actual;
+    }
+    if (!(isfinite(psum) && fabs(psum - 1.0) <= 3.0e-4)) valid = 0;
+    if (deterministic) {
+      /* llama2c_common.h:150-190, float arithmetic. */
+      const float fscale = 1.0f / sqrtf((float)(ss / size) + eps);
+      float fmx = -FLT_MAX;
+      double fes = 0.0, fsum = 0.0;
+      for (j = 0; j < size; ++j) fmx = fmaxf(fmx, x[j]);
+      for (j = 0; j < size; ++j) fes += exp((double)(x[j] - fmx));
+      for (j = 0; j < size; ++j) {
+        const float fe = x[j] * fscale * weight[j];
+        const float fp = (float)(exp((double)(x[j] - fmx)) / fes);
+        if (!(fabsf(normalized[off + j] - fe) <= 3.0e-4f)) valid = 0;
+        if (!(fabsf(softmax[off + j] - fp) <= 1.0e-9f + 1.0e-3f * fabsf(fp))) valid = 0;
+        if (!isfinite(softmax[off + j]) || softmax[off + j] <= 0.0f) valid = 0;
+        fsum += softmax[off + j];
+      }
+      if (!(isfinite(fsum) && fabs(fsum - 1.0) <= 3.0e-4)) valid = 0;
+    }
+  }
+  if (err) {
+    err[0] = e0;
+    err[1] = e1;
+    err[2] = e2;
+    err[3] = e3;
+  }
+  return valid;
+}
+
+/*
+ * Double reference, magnitude sum and tolerance of out[b][r] = sum_c W[r][c] x[b][c]
+ * for the listed vectors b (llama2c_common.h:277-294; vector 0 only for the
+ * reference's matrix-vector product). product is indexed [b * rows + r] when
+ * batched is 1, [r] otherwise. Writes the tolerance (float, clipped to 1e-4
+ * for deterministic inputs as :311-317 does) and the double reference; returns
+ * 1 when every checked element is within its tolerance (and, for
+ * deterministic inputs, within 1e-4 of input[b][r % size]).
+ */
+int orc_product_check(int deterministic, int batched, const float *x, const float *W,
+                      const float *product, int batch, int size, int rows, const int *vectors,
+                      int nvectors, float *tolerance, double *reference, double *max_ratio,
+                      double *max_rel) {
+  int valid = 1, v, r, c;
+  const double gamma = orc_gamma(size);
+  double mr = 0.0, ml = 0.0;
+  (void)batch;
+  for (v = 0; v < nvectors; ++v) {
+    const int b = vectors[v];
+    const float *xb = x + (size_t)b * size;
+    for (r = 0; r < rows; ++r) {
+      const float *w = W + (size_t)r * size;
+      const size_t at = batched ? (size_t)b * rows + r : (size_t)r;
+      double sum = 0.0, mag = 0.0, tol, d;
+      for (c = 0; c < size; ++c) {
+        const double term = (double)w[c] * xb[c];
+        sum += term;
+        mag += fabs(term);
+      }
+      tol = gamma * mag + FLT_MIN;
+      d = fabs(product[at] - sum);
+      if (!(d <= tol)) valid = 0;
+      if (d != d) d = INFINITY;
+      if (d / tol > mr) mr = d / tol;
+      if ((mag > 0 ? d / mag : d) > ml) ml = mag > 0 ? d / mag : d;
+      tolerance[at] = (float)tol;
+      reference[at] = sum;
+      if (deterministic) {
+        if (!(fabsf(product[at] - xb[r % size]) <= 1.0e-4f)) valid = 0;
+        tolerance[at] = fminf(tolerance[at], 1.0e-4f);
+      }
+    }
+  }
+  if (max_ratio) *max_ratio = mr;
+  if (max_rel) *max_rel = ml;
+  return valid;
+}
+
+/* ------------------------------------------------------------------------ */
+/* fp32 CPU iteration in llama2.c's loop order (karpathy/llama2.c run.c      */
+/* rmsnorm / softmax / matmul as restated in the decoder contract,           */
+/* applications/loom_private/decoder/contract.json:68): the CPU port timed   */
+/* as the baseline. matmul_batched = 0 multiplies vector 0 only.             */
+
+void orc_iteration_f32(const float *input, const float *probabilities, const float *weight,
+                       const float *matrix, int batch, int size, int rows, int matmul_batched,
+                       int matmul_vectors, float *normalized, float *softmax, float *product) {
+  int b, j, r;
+  for (b = 0; b < batch; ++b) {
+    const float *x = input + (size_t)b * size;
+    float *o = normalized + (size_t)b * size;
+    float ss = 0.0f;
+    for (j = 0; j < size; ++j) ss += x[j] * x[j];
+    ss /= (float)size;
+    ss += 1e-5f;
+    ss = 1.0f / sqrtf(ss);
+    for (j = 0; j < size; ++j) o[j] = weight[j] * (ss * x[j]);
+  }
+  for (b = 0; b < batch; ++b) {
+    const float *p = probabilities + (size_t)b * size;
+    float *o = softmax + (size_t)b * size;
+    float mx = p[0], sum = 0.0f;
+    for (j = 1; j < size; ++j)
+      if (p[j] > mx) mx = p[j];
+    for (j = 0; j < size; ++j) {
+      o[j] = expf(p[j] - mx);
+      sum += o[j];
+    }
+    for (j = 0; j < size; ++j) o[j] /= sum;
+  }
+  {
+    const int nv = matmul_batched ? matmul_vectors : 1;
+    for (b = 0; b < nv; ++b) {
+      const float *x = input + (size_t)b * size;
+      for (r = 0; r < rows; ++r) {
+        const float *w = matrix + (size_t)r * size;
+        float val = 0.0f;
+        for (j = 0; j < size; ++j) val += w[j] * x[j];
+        product[matmul_batched ? (size_t)b * rows + r : (size_t)r] = val;
+      }
+    }
+  }
+}
+
+/* The naive kernel's arithmetic: one fmaf per column in column order
+ * (llama2c/llama2c_cuda_graph.cu:119-128, with the multiply-add contracted as
+ * nvcc contracts it). */
+void orc_matvec_fma(const float *x, const float *W, int cols, int rows, float *out) {
+  int r, c;
+  for (r = 0; r < rows; ++r) {
+    const float *w = W + (size_t)r * cols;
+    float acc = 0.0f;
+    for (c = 0; c < cols; ++c) acc = fmaf(x[c], w[c], acc);
+    out[r] = acc;
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Formats: experiments/blackwell/lowprec/spec.json:20-27 and                */
+/* reference.cpp:13-96, restated by brute force over all codes.              */
+
+static double e2m1_mag(unsigned c) {
+  static const double m[8] = {0, 0.5, 1, 1.5, 2, 3, 4, 6};
+  return m[c & 7u];
+}
+
+double orc_e2m1_value(unsigned code) { return (code & 8u) ? -e2m1_mag(code) : e2m1_mag(code); }
+
+/* Nearest of the 8 magnitudes; a tie goes to the code whose least significant
+ * bit is 0; above 6 saturates; a zero magnitude is +0. */
+unsigned orc_e2m1_encode(double v) {
+  const double a = fabs(v);
+  unsigned best = 0, c;
+  if (a >= 6.0) return v < 0 ? 15u : 7u; /* saturation (distances lose precision far out) */
+  for (c = 1; c < 8; ++c) {
+    const double dc = fabs(a - e2m1_mag(c)), db = fabs(a - e2m1_mag(best));
+    if (dc < db || (dc == db && (best & 1u) && !(c & 1u))) best = c;
+  }
+  return (best != 0 && v < 0) ? (best | 8u) : best;
+}
+
+double orc_ue4m3_value(unsigned code) {
+  const unsigned e = (code >> 3) & 15u, m = code & 7u;
+  return e == 0 ? ldexp(m / 8.0, -6) : ldexp(1.0 + m / 8.0, (int)e - 7);
+}
+
+/* OCP e4m3 magnitude codes 0..126 (0x7f is NaN), nearest with ties to the
+ * even code, saturating at 448; bit 7 is the sign (the reference's UE4M3
+ * table plus a sign bit). */
+unsigned orc_ue4m3_encode(double v) {
+  const double a = fabs(v);
+  unsigned best = 0, c;
+  if (a >= 448.0) return v < 0 ? 0xfeu : 0x7eu; /* saturation */
+  for (c = 1; c <= 126; ++c) {
+    const double dc = fabs(a - orc_ue4m3_value(c)), db = fabs(a - orc_ue4m3_value(best));
+    if (dc < db || (dc == db && (best & 1u) && !(c & 1u))) best = c;
+  }
+  return (best != 0 && v < 0) ? (best | 0x80u) : best;
+}
+
+/* bf16 round to nearest even: compare the two neighbours exactly in double. */
+uint16_t orc_bf16(float v) {
+  uint32_t bits, lo_bits, hi_bits;
+  float lo, hi;
+  double dl, dh;
+  memcpy(&bits, &v, 4);
+  if ((bits & 0xffffu) == 0) return (uint16_t)(bits >> 16);
+  lo_bits = bits & 0xffff0000u;
+  hi_bits = lo_bits + 0x10000u;
+  memcpy(&lo, &lo_bits, 4);
+  memcpy(&hi, &hi_bits, 4);
+  dl = fabs((double)v - lo);
+  dh = fabs((double)hi - v);
+  if (dl < dh) return (uint16_t)(lo_bits >> 16);
+  if (dh < dl) return (uint16_t)(hi_bits >> 16);
+  return ((lo_bits >> 16) & 1u) ? (uint16_t)(hi_bits >> 16) : (uint16_t)(lo_bits >> 16);
+}
+
+/* Largest X with 6 * 2^X <= amax (= floor(log2(amax / 6))), clamped to
+ * [-127, 127]; -127 for amax = 0. Found by stepping X, exact in double. */
+int orc_mxfp4_exponent(float amax) {
+  int x = -127;
+  if (!(amax > 0.0f)) return -127;
+  while (x < 127 && ldexp(6.0, x + 1) <= (double)amax) ++x;
+  return x;
+}
+
+/* One row: codes (one byte per element, unpacked) and scale codes. */
+void orc_quantize_mxfp4_row(const float *w, int cols, uint8_t *codes, uint8_t *scales) {
+  int blk, i;
+  for (blk = 0; blk * 32 < cols; ++blk) {
+    float amax = 0.0f;
+    int x;
+    for (i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(w[blk * 32 + i]));
+    x = orc_mxfp4_exponent(amax);
+    scales[blk] = (uint8_t)(x + 127);
+    for (i = 0; i < 32; ++i)
+      codes[blk * 32 + i] = amax > 0.0f ? (uint8_t)orc_e2m1_encode(ldexp((double)w[blk * 32 + i], -x)) : 0;
+  }
+}
+
+/* Per-row fp8: scale = amax / 448 in float (1 when amax = 0), code =
+ * e4m3(w / scale) in float. */
+float orc_quantize_fp8_row(const float *w, int cols, uint8_t *codes) {
+  float amax = 0.0f, scale;
+  int k;
+  for (k = 0; k < cols; ++k) amax = fmaxf(amax, fabsf(w[k]));
+  scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+  for (k = 0; k < cols; ++k) {
+    const float q = w[k] / scale;
+    codes[k] = (uint8_t)orc_ue4m3_encode(q);
+  }
+  return scale;
+}
+
+/* Dequantize-then-fp32 reference of the quantized product for the listed
+ * vectors: deq = value(code) * scale in float, then a double dot product with
+ * the bf16 activations. out is [b * rows + r]; mag receives sum |terms|. */
+void orc_qmatmul_ref(int fmt, const uint16_t *xbf16, const uint8_t *codes, const void *scales,
+                     int size, int rows, const int *vectors, int nvectors, double *out,
+                     double *mag) {
+  int v, r, k;
+  float *w = (float *)malloc((size_t)size * sizeof(float));
+  for (r = 0; r < rows; ++r) {
+    for (k = 0; k < size; ++k) {
+      if (fmt == 0) {
+        const uint8_t byte = codes[(size_t)r * (size / 2) + k / 2];
+        const unsigned c = (byte >> (4 * (k % 2))) & 15u;
+        const uint8_t s = ((const uint8_t *)scales)[(size_t)r * (size / 32) + k / 32];
+        w[k] = (float)orc_e2m1_value(c) * ldexpf(1.0f, (int)s - 127);
+      } else {
+        const uint8_t c = codes[(size_t)r * size + k];
+        const float val = (float)((c & 0x80u) ? -orc_ue4m3_value(c & 0x7fu) : orc_ue4m3_value(c));
+        w[k] = val * ((const float *)scales)[r];
+      }
+    }
+    for (v = 0; v < nvectors; ++v) {
+      const int b = vectors[v];
+      double s = 0.0, m = 0.0;
+      for (k = 0; k < size; ++k) {
+        uint32_t bits = (uint32_t)xbf16[(size_t)b * size + k] << 16;
+        float xv;
+        memcpy(&xv, &bits, 4);
+        s += (double)xv * w[k];
+        m += fabs((double)xv * w[k]);
+      }
+      out[(size_t)b * rows + r] = s;
+      if (mag) mag[(size_t)b * rows + r] = m;
+    }
+  }
+  free(w);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Array forms for callers that cross a foreign-function boundary.           */
+
+void orc_uniform_array(uint64_t seed, uint64_t stream, uint64_t start, size_t n, float *out) {
+  size_t i;
+  for (i = 0; i < n; ++i) out[i] = orc_uniform(seed, stream, start + i);
+}
+
+void orc_normal_array(uint64_t seed, uint64_t stream, uint64_t start, size_t n, float *out) {
+  size_t i;
+  for (i = 0; i < n; ++i) out[i] = orc_normal(seed, stream, start + i);
+}
+
+void orc_e2m1_encode_array(const double *v, size_t n, uint8_t *out) {
+  size_t i;
+  for (i = 0; i < n; ++i) out[i] = (uint8_t)orc_e2m1_encode(v[i]);
+}
+
+void orc_ue4m3_encode_array(const double *v, size_t n, uint8_t *out) {
+  size_t i;
+  for (i = 0; i < n; ++i) out[i] = (uint8_t)orc_ue4m3_encode(v[i]);
+}
+
+void orc_bf16_array(const float *v, size_t n, uint16_t *out) {
+  size_t i;
+  for (i = 0; i < n; ++i) out[i] = orc_bf16(v[i]);
+}
+
+void orc_mxfp4_exponent_array(const float *v, size_t n, int *out) {
+  size_t i;
+  for (i = 0; i < n; ++i) out[i] = orc_mxfp4_exponent(v[i]);
+}
+
+void orc_quantize_mxfp4(const float *W, int rows, int cols, uint8_t *codes, uint8_t *scales) {
+  int r;
+  for (r = 0; r < rows; ++r)
+    orc_quantize_mxfp4_row(W + (size_t)r * cols, cols, codes + (size_t)r * cols,
+                           scales + (size_t)r * (cols / 32));
+}
+
+void orc_quantize_fp8(const float *W, int rows, int cols, uint8_t *codes, float *scales) {
+  int r;
+  for (r = 0; r < rows; ++r)
+    scales[r] = orc_quantize_fp8_row(W + (size_t)r * cols, cols, codes + (size_t)r * cols);
+}
