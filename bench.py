@@ -1,0 +1,199 @@
+"""Benchmark of the llama2c hot path on one MI355X.
+
+One "step" is one llama2c iteration of the harness (rmsnorm | softmax |
+matmul on three streams, joined) over device-resident synthetic inputs. The
+headline workload is the largest profiled shape, batch 1024 x dim 16384 x rows
+8192, with the batched fp32 contraction on the matrix cores, replayed as a
+hipGraph, no copies: `value` is its microseconds per iteration (lower is
+better). The other benchmark configurations (decode GEMV 1 x 4096 x 11008,
+launch-bound 8 x 768 x 2048, the reference-compatible GEMV iteration at the
+large shape, the fused single launch, and the MXFP4 / fp8 weights) and the
+graph/direct and copy/nocopy splits are reported under "lines".
+
+The harness runs in this process (libl2c_host.so via ctypes): HIP events on
+each operation's own stream time the kernels, so `roofline` comes from the
+same run. cpu_baseline times the oracle's fp32 CPU iteration (llama2.c loop
+order) on this host over a bounded sample of the headline shape and scales it
+to one whole iteration.
+
+Usage: python bench.py [--gpus N] [--steps K] [--warmup W] [--quick]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "cuda-elastic_amd"))
+
+HBM_PEAK_GBPS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_f32_mfma_c4_traffic.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def run_line(l2c, args):
+    t = time.time()
+    code, rec, raw = l2c.harness(args)
+    log(f"[bench] {' '.join(map(str, args))} -> exit {code} in {time.time() - t:.1f}s: "
+        f"gpu_ms_per_iter={rec.get('gpu_ms_per_iter')} valid={rec.get('valid')}")
+    if code != 0 or rec.get("valid") != 1:
+        raise SystemExit(f"harness run failed (exit {code}): {raw}")
+    return rec
+
+
+def summarize(name, rec):
+    out = {
+        "name": name, "mode": rec["mode"], "matmul": rec["matmul"], "batch": rec["batch"],
+        "size": rec["size"], "rows": rec["rows"], "copies": rec["copies"],
+        "launches": rec["launches"], "us_per_iter": rec["gpu_ms_per_iter"] * 1000.0,
+        "single_us": rec["single_us"], "submit_us_per_iter": rec["submit_us_per_iter"],
+        "achieved_gbps": rec["achieved_gbps"], "valid": rec["valid"],
+        "strict_valid": rec["strict_valid"],
+        "rms_us": rec["rms_us"], "rms_gbps": rec["rms_gbps"], "rms_hbm_frac": rec["rms_hbm_frac"],
+        "softmax_us": rec["softmax_us"], "softmax_gbps": rec["softmax_gbps"],
+        "softmax_hbm_frac": rec["softmax_hbm_frac"], "matmul_us": rec["matmul_us"],
+        "matmul_gbps": rec["matmul_gbps"], "matmul_tflops": rec["matmul_tflops"],
+        "matmul_bound": rec["matmul_bound"], "matmul_frac": rec["matmul_frac"],
+        "rms_max_rel_err": rec["rms_max_rel_err"], "softmax_max_rel_err": rec["softmax_max_rel_err"],
+        "product_max_rel_err": rec["product_max_rel_err"],
+    }
+    if rec["mode"] == "graph":
+        out["graph_capture_ms"] = rec["graph_capture_ms"]
+        out["graph_instantiate_ms"] = rec["graph_instantiate_ms"]
+    return out
+
+
+def cpu_baseline(batch, size, rows, sample_vectors, sample_rows_norm):
+    """The oracle's fp32 iteration (llama2.c loop order, one thread) on a
+    bounded sample, scaled to one whole iteration of batch x size x rows."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle
+
+    L = oracle.lib()
+    inp = oracle.fill("scaled", 1, sample_rows_norm, size, rows)
+    f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+    n = np.empty(sample_rows_norm * size, np.float32)
+    s = np.empty(sample_rows_norm * size, np.float32)
+    p = np.empty(sample_rows_norm * rows, np.float32)
+    # rmsnorm + softmax over sample_rows_norm vectors, no product.
+    t0 = time.perf_counter()
+    L.orc_iteration_f32(inp.input, inp.probabilities, inp.weight, inp.matrix, sample_rows_norm, size,
+                        0, 1, 0, n, s, p)
+    t_vec = time.perf_counter() - t0
+    # The product of sample_vectors vectors against all rows (batched order).
+    t0 = time.perf_counter()
+    L.orc_iteration_f32(inp.input, inp.probabilities, inp.weight, inp.matrix, 0, size, rows, 1,
+                        sample_vectors, n, s, p)
+    t_mm = time.perf_counter() - t0
+    per_iter_s = t_vec * batch / sample_rows_norm + t_mm * batch / sample_vectors
+    return {
+        "value": per_iter_s * 1e6, "unit": "us/iter", "cores": 1, "kind": "port",
+        "sample": (f"oracle orc_iteration_f32 (fp32, llama2.c loop order, 1 thread): rmsnorm+softmax "
+                   f"of {sample_rows_norm} of {batch} vectors ({t_vec:.2f} s) and the product of "
+                   f"{sample_vectors} of {batch} vectors x {rows} rows x {size} ({t_mm:.2f} s), "
+                   f"scaled linearly to one {batch}x{size}x{rows} iteration"),
+        "measured_s": t_vec + t_mm,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline and cpu baseline only")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported on this build "
+              "(every GPU box has one MI355X; see DESIGN.md for how the path would shard)",
+              file=sys.stderr)
+        return 2
+    import l2c
+
+    l2c.load_host()
+    K, W = args.steps, args.warmup
+    B, S, R = 1024, 16384, 8192
+
+    def cfg(mode, launches, batch, size, rows, copies, matmul, inputs="scaled=1", warm=W, extra=()):
+        return [mode, launches, batch, size, rows, 1, 1, copies, matmul, inputs,
+                f"warmup_iters={warm}", *extra]
+
+    headline = run_line(l2c, cfg("graph", K, B, S, R, "nocopy", "batched"))
+    lines = [summarize("c4_batched_graph_nocopy", headline)]
+    if not args.quick:
+        plan = [
+            ("c4_batched_direct_nocopy", cfg("direct", K, B, S, R, "nocopy", "batched")),
+            ("c4_batched_graph_copy", cfg("graph", K, B, S, R, "copy", "batched")),
+            ("c4_batched_direct_copy", cfg("direct", K, B, S, R, "copy", "batched")),
+            ("c4_gemv_graph_nocopy", cfg("graph", 200, B, S, R, "nocopy", "coalesced")),
+            ("c4_gemv_direct_nocopy", cfg("direct", 200, B, S, R, "nocopy", "coalesced")),
+            ("c4_fused_graph_nocopy", cfg("graph", 200, B, S, R, "nocopy", "fused")),
+            ("c2_gemv_graph_nocopy", cfg("graph", 1000, 1, 4096, 11008, "nocopy", "coalesced", warm=50)),
+            ("c2_gemv_direct_nocopy", cfg("direct", 1000, 1, 4096, 11008, "nocopy", "coalesced", warm=50)),
+            ("c3_graph_nocopy", cfg("graph", 10000, 8, 768, 2048, "nocopy", "coalesced", warm=100)),
+            ("c3_direct_nocopy", cfg("direct", 10000, 8, 768, 2048, "nocopy", "coalesced", warm=100)),
+            ("c3_graph_copy", cfg("graph", 10000, 8, 768, 2048, "copy", "coalesced", warm=100)),
+            ("c3_direct_copy", cfg("direct", 10000, 8, 768, 2048, "copy", "coalesced", warm=100)),
+            ("c5_mxfp4_graph_nocopy", cfg("graph", K, B, S, R, "nocopy", "mxfp4", inputs="normal=1")),
+            ("c5_fp8_graph_nocopy", cfg("graph", K, B, S, R, "nocopy", "fp8", inputs="normal=1")),
+        ]
+        for name, a in plan:
+            lines.append(summarize(name, run_line(l2c, a)))
+
+    gemm_us = headline["matmul_us"]
+    flops = 2.0 * B * R * S
+    achieved = flops / (gemm_us * 1e-6) / 1e12
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        try:
+            traffic = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    roofline = {
+        "kernel": "gemm_f32_mfma_kernel (l2c_matmul, v_mfma_f32_32x32x2_f32)",
+        "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+        "frac": achieved / FP32_MFMA_PEAK_TFLOPS, "traffic": traffic,
+        "algorithmic_flops_per_launch": flops,
+        "avg_launch_us": gemm_us,
+        "timing": "HIP events on the matmul stream around K launches of l2c_matmul alone",
+    }
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(B, S, R, sample_vectors=48, sample_rows_norm=256)
+        log(f"[bench] cpu baseline {cpu['value'] / 1e6:.1f} s/iter ({cpu['measured_s']:.1f} s measured)")
+        cpu.pop("measured_s")
+    us = headline["gpu_ms_per_iter"] * 1000.0
+    result = {
+        "metric": "us/iter (llama2c iteration: rmsnorm + softmax + batched fp32 W.x on MFMA), hipGraph",
+        "value": us, "unit": "us/iter", "n_gpus": 1, "steps": headline["launches"], "warmup": W,
+        "ms_per_step": headline["gpu_ms_per_iter"], "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: seeded splitmix64 inputs, scaled distributions (x,logits U[-1,1), "
+                "weight U[0.5,1.5), W U[-1/128,1/128)), device-resident",
+        "config": {"workload": "C4 llama2c iteration, batch 1024 x dim 16384 x rows 8192, batched "
+                               "fp32 matmul on matrix cores, hipGraph replay, no copies",
+                   "batch": B, "size": S, "rows": R, "mode": "graph", "copies": 0,
+                   "matmul": "batched", "iteration_flops": flops,
+                   "iteration_min_bytes": headline["min_bytes_per_iter"]},
+        "tflops": headline["matmul_tflops"],
+        "rms_gbps": headline["rms_gbps"], "softmax_gbps": headline["softmax_gbps"],
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "lines": lines,
+        "device": headline.get("device"),
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -57,7 +57,8 @@ std::string usage_text(const char *program) {
   text +=
       " [graph|direct] [launches|auto] [batch] [size] [rows] [repeats] [warmup_ms]"
       " [copy|nocopy] [naive|coalesced|fused|batched|mxfp4|fp8]"
-      " [deterministic|random[=SEED]|scaled[=SEED]|normal[=SEED]] [fullcheck] [--dump=FILE]\n";
+      " [deterministic|random[=SEED]|scaled[=SEED]|normal[=SEED]] [fullcheck] [warmup_iters=N]"
+      " [--dump=FILE]\n";
   return text;
 }
 
@@ -146,6 +147,10 @@ bool parse_options(int argc, const char *const *argv, Options *options, std::str
       break;
     }
     if (matched) continue;
+    if (std::strncmp(arg, "warmup_iters=", 13) == 0) {
+      if (!positive_int(arg + 13, &options->warmup_iters)) return false;
+      continue;
+    }
     if (positional == 0 && std::strcmp(arg, "auto") == 0) {
       options->auto_launches = true;
       ++positional;

@@ -60,6 +60,7 @@ struct Options {
   Matmul matmul = Matmul::kNaive;
   bool auto_launches = false;
   bool full_check = false;  // validate every (b, r) of a batched product
+  int warmup_iters = 0;     // > 0: exactly this many warm-up iterations instead of warmup_ms
   int device = 0;
   InputOptions inputs;
 };

@@ -355,7 +355,7 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
       range_pop();
       synchronize_all();
       ++warm;
-    } while (ms_since(warm_start) < o.warmup_ms);
+    } while (o.warmup_iters > 0 ? warm < o.warmup_iters : ms_since(warm_start) < o.warmup_ms);
     res->warmup_iterations = warm;
     int launches = o.launches;
     if (o.auto_launches) {

@@ -1,0 +1,144 @@
+"""The drop-in harness on the GPU: the reference's check matrix
+(llama2c/Makefile:24-28,44-56: shapes x inputs x graph/direct x copy/nocopy,
+every run exit 0 and valid=1), extended to this build's variants, and the
+dump compare flow of llama2c/compare_sota.sh:41-71 (graph, direct and fused
+dumps on identical inputs must match within the oracle tolerances), with the
+oracle re-checking every dump independently."""
+import math
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SMALL = [(64, 1000, 300, 1), (33, 1001, 77, 2)]   # batch size rows repeats
+VARIANTS = ["naive", "coalesced", "fused", "batched"]
+
+
+def run(l2c, args):
+    code, rec, raw = l2c.harness([str(a) for a in args])
+    return code, rec, raw
+
+
+@pytest.mark.parametrize("shape", SMALL, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("inputs", ["deterministic", "random=1", "random=2", "scaled=3"])
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_check_matrix_small(l2c, shape, inputs, variant):
+    batch, size, rows, repeats = shape
+    for mode in ("graph", "direct"):
+        for copies in ("nocopy", "copy"):
+            args = [mode, "auto", batch, size, rows, repeats, 5, copies, variant, inputs]
+            print("case", " ".join(map(str, args)), flush=True)
+            code, rec, raw = run(l2c, args)
+            assert code == 0 and rec["valid"] == 1, raw
+            assert rec["strict_valid"] == 1, raw
+            assert rec["batch"] == batch and rec["size"] == size and rec["rows"] == rows
+            assert rec["launches"] >= 20 and rec["inputs"] == inputs.split("=")[0]
+
+
+@pytest.mark.parametrize("variant", ["coalesced", "batched", "fused", "naive"])
+def test_sheet_shape(l2c, variant):
+    """The sheet shape 1024 x 16384 x 8192 in graph and direct mode."""
+    for mode, copies in (("graph", "nocopy"), ("direct", "copy")):
+        args = [mode, 3, 1024, 16384, 8192, 1, 1, copies, variant, "random=1"]
+        print("case", " ".join(map(str, args)), flush=True)
+        code, rec, raw = run(l2c, args)
+        assert code == 0 and rec["valid"] == 1, raw
+        assert rec["strict_valid"] == 1, raw
+
+
+@pytest.mark.parametrize("variant,inputs", [("mxfp4", "normal=1"), ("fp8", "normal=2"),
+                                            ("mxfp4", "scaled=1"), ("fp8", "random=3")])
+def test_quantized_variants(l2c, variant, inputs):
+    for mode, copies in (("graph", "nocopy"), ("direct", "copy")):
+        args = [mode, 3, 256, 4096, 512, 1, 1, copies, variant, inputs]
+        code, rec, raw = run(l2c, args)
+        assert code == 0 and rec["valid"] == 1 and rec["strict_valid"] == 1, raw
+
+
+def _oracle_recheck(orc, dump, mode_name, seed):
+    """Regenerates the inputs and re-validates a dump with the oracle."""
+    b, s, r = dump["batch"], dump["size"], dump["rows"]
+    inp = orc.fill(mode_name, seed, b, s, r)
+    ok, err = orc.check_vectors(mode_name == "deterministic", inp, dump["normalized"], dump["softmax"], b, s)
+    assert ok and err[1] <= 1e-5 and err[3] <= 1e-5, err
+    batched = dump["magic"] == "L2CDUMP2"
+    vectors = list(range(b)) if batched else [0]
+    ok, tol, refv, ratio, rel = orc.product_check(mode_name == "deterministic", batched, inp.input,
+                                                  inp.matrix, dump["product"], b, s, r, vectors)
+    assert ok, ratio
+    assert rel <= 1e-4 * math.sqrt(s)
+    # The harness's own tolerance and reference sections equal the oracle's.
+    np.testing.assert_array_equal(dump["product_tolerance"], tol)
+    np.testing.assert_array_equal(dump["product_reference"], refv)
+
+
+@pytest.mark.parametrize("shape", [(64, 1000, 300), (33, 1001, 77), (1024, 16384, 8192)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("inputs", ["deterministic", "random=1", "random=2", "random=3"])
+def test_compare_flow(l2c, orc, tmp_path, shape, inputs):
+    if shape[0] == 1024 and inputs not in ("random=1", "deterministic"):
+        pytest.skip("the sheet shape runs two input sets to bound the run time")
+    batch, size, rows = shape
+    dumps = []
+    for label, mode, variant in (("graph", "graph", "coalesced"), ("direct", "direct", "coalesced"),
+                                 ("fused", "graph", "fused"), ("naive", "direct", "naive")):
+        path = str(tmp_path / f"{label}.bin")
+        args = [mode, 3, batch, size, rows, 1, 1, "nocopy", variant, inputs, f"--dump={path}"]
+        print("case", " ".join(map(str, args)), flush=True)
+        code, rec, raw = run(l2c, args)
+        assert code == 0 and rec["valid"] == 1, raw
+        dumps.append(path)
+    code, out = l2c.compare_dumps(dumps)
+    print(out)
+    assert code == 0, out
+    name = inputs.split("=")[0]
+    seed = int(inputs.split("=")[1]) if "=" in inputs else 0
+    if batch * size <= 1 << 20:
+        for p in dumps:
+            _oracle_recheck(orc, orc.read_dump(p), name, seed)
+
+
+def test_batched_dump_and_compare(l2c, orc, tmp_path):
+    paths = []
+    for mode in ("graph", "direct"):
+        path = str(tmp_path / f"b_{mode}.bin")
+        code, rec, raw = run(l2c, [mode, 3, 96, 640, 200, 1, 1, "nocopy", "batched", "scaled=4",
+                                   f"--dump={path}"])
+        assert code == 0 and rec["valid"] == 1, raw
+        paths.append(path)
+    code, out = l2c.compare_dumps(paths)
+    assert code == 0, out
+    _oracle_recheck(orc, orc.read_dump(paths[0]), "scaled", 4)
+
+
+def test_dump_env_variable(l2c, tmp_path, monkeypatch):
+    path = str(tmp_path / "env.bin")
+    monkeypatch.setenv("LLAMA2C_DUMP", path)
+    code, rec, raw = l2c.harness(["direct", 3, 4, 64, 16, 1, 1, "nocopy", "coalesced", "random=5"],
+                                 in_process=False)
+    assert code == 0 and os.path.exists(path), raw
+
+
+def test_unwritable_dump_fails(l2c):
+    code, rec, raw = l2c.harness(["direct", 3, 4, 64, 16, 1, 1, "nocopy", "coalesced",
+                                  "--dump=/nonexistent-dir/x.bin"], in_process=False)
+    assert code == 1 and rec.get("valid") == 0, raw
+    assert "cannot open dump file" in raw
+
+
+def test_executable_line_format(l2c):
+    """The standalone executable prints exactly one line whose leading keys are
+    the reference's, in its order (llama2c/llama2c_cuda_graph.cu:508-517)."""
+    keys = ("mode matmul launches batch size rows repeats copies warmup_ms warmup_iterations gpu_ms "
+            "gpu_ms_per_iter single_iterations single_us wall_ms wall_ms_per_iter submit_us "
+            "submit_us_per_iter graph_capture_ms graph_instantiate_ms graph_upload_ms rms_waves "
+            "softmax_waves matmul_waves min_waves min_bytes_per_iter achieved_gbps valid inputs seed").split()
+    code, rec, raw = l2c.harness(["graph", 20, 8, 768, 2048, 1, 5, "copy", "coalesced", "random=1"],
+                                 in_process=False)
+    assert code == 0, raw
+    line = raw.splitlines()[0]
+    got = [t.split("=")[0] for t in line.split()][:len(keys)]
+    assert got == keys
+    assert rec["min_bytes_per_iter"] == 2 * 8 * 768 * 4 + 768 * 4 + 2 * 8 * 768 * 4 + 2048 * 768 * 4 + (768 + 2048) * 4
