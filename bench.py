@@ -168,7 +168,7 @@ def main():
     }
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(B, S, R, sample_vectors=48, sample_rows_norm=256)
+        cpu = cpu_baseline(B, S, R, sample_vectors=192, sample_rows_norm=512)
         log(f"[bench] cpu baseline {cpu['value'] / 1e6:.1f} s/iter ({cpu['measured_s']:.1f} s measured)")
         cpu.pop("measured_s")
     us = headline["gpu_ms_per_iter"] * 1000.0

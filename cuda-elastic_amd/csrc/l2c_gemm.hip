@@ -60,20 +60,23 @@ struct Smem {
   float b[2][kBN][kLdsStride];
 };
 
-// Loads one float4 of a K-contiguous operand row, zero outside [0, rows) x [0, K).
+// Loads one float4 of a K-contiguous operand row; zero outside
+// [0, rows) x [0, K). Branch-free: the address is clamped into the operand
+// and the value replaced afterwards, so every lane issues its load.
 template <bool VEC>
 __device__ __forceinline__ float4 load_chunk(const float *base, int row, int rows, int k, int K) {
-  if (row >= rows) return make_float4(0.f, 0.f, 0.f, 0.f);
-  const float *p = base + static_cast<size_t>(row) * K + k;
+  const bool row_ok = row < rows;
+  const float *p = base + static_cast<size_t>(row_ok ? row : rows - 1) * K;
   if constexpr (VEC) {
-    if (k < K) return *reinterpret_cast<const float4 *>(p);
-    return make_float4(0.f, 0.f, 0.f, 0.f);
+    const bool ok = row_ok && k < K;
+    const float4 v = *reinterpret_cast<const float4 *>(p + (k < K ? k : K - 4));
+    return ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
   } else {
     float4 v;
-    v.x = k < K ? p[0] : 0.f;
-    v.y = k + 1 < K ? p[1] : 0.f;
-    v.z = k + 2 < K ? p[2] : 0.f;
-    v.w = k + 3 < K ? p[3] : 0.f;
+    v.x = row_ok && k < K ? p[k] : 0.f;
+    v.y = row_ok && k + 1 < K ? p[k + 1] : 0.f;
+    v.z = row_ok && k + 2 < K ? p[k + 2] : 0.f;
+    v.w = row_ok && k + 3 < K ? p[k + 3] : 0.f;
     return v;
   }
 }
@@ -83,7 +86,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_mfma_kernel(float *__restri
                                                                  const float *__restrict__ X,
                                                                  const float *__restrict__ W,
                                                                  int M, int N, int K) {
-  __shared__ Smem sm;
+  __shared__ __attribute__((aligned(16))) Smem sm;
 
   // XCD-aware tile order (see the file header).
   int tile = blockIdx.x;
@@ -138,48 +141,61 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_mfma_kernel(float *__restri
   const int frag_row = lane % 32;
   const int frag_k = 4 * (lane / 32);
   const int nk = (K + kBK - 1) / kBK;
+  const float *a_base = &sm.a[0][wm * kWaveM + frag_row][frag_k];
+  const float *b_base = &sm.b[0][wn * kWaveN + frag_row][frag_k];
+  constexpr int kABuf = kBM * kLdsStride, kBBuf = kBN * kLdsStride;
+
+  // Fragments of one 8-deep k group (one ds_read_b128 per operand block).
+  float4 fa[2][kFragM], fb[2][kFragN];
+  auto load_frags = [&](int slot, int buf, int kk) {
+#pragma unroll
+    for (int i = 0; i < kFragM; ++i)
+      fa[slot][i] = *reinterpret_cast<const float4 *>(a_base + buf * kABuf + i * 32 * kLdsStride + kk);
+#pragma unroll
+    for (int j = 0; j < kFragN; ++j)
+      fb[slot][j] = *reinterpret_cast<const float4 *>(b_base + buf * kBBuf + j * 32 * kLdsStride + kk);
+  };
+  auto mfma_group = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < kFragM; ++i)
+#pragma unroll
+      for (int j = 0; j < kFragN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[slot][i].x, fb[slot][j].x, acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < kFragM; ++i)
+#pragma unroll
+      for (int j = 0; j < kFragN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[slot][i].y, fb[slot][j].y, acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < kFragM; ++i)
+#pragma unroll
+      for (int j = 0; j < kFragN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[slot][i].z, fb[slot][j].z, acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < kFragM; ++i)
+#pragma unroll
+      for (int j = 0; j < kFragN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[slot][i].w, fb[slot][j].w, acc[i][j], 0, 0, 0);
+  };
 
   global_load(0);
   lds_store(0);
   __syncthreads();
+  load_frags(0, 0, 0);
 
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < nk) global_load((kt + 1) * kBK);
+    const bool more = kt + 1 < nk;
+    if (more) global_load((kt + 1) * kBK);
+    // Fragments for group g + 1 are read while group g's MFMAs run.
 #pragma unroll
-    for (int kk = 0; kk < kBK; kk += 8) {
-      float4 a[kFragM], b[kFragN];
-#pragma unroll
-      for (int i = 0; i < kFragM; ++i)
-        a[i] = *reinterpret_cast<const float4 *>(
-            &sm.a[buf][wm * kWaveM + i * 32 + frag_row][kk + frag_k]);
-#pragma unroll
-      for (int j = 0; j < kFragN; ++j)
-        b[j] = *reinterpret_cast<const float4 *>(
-            &sm.b[buf][wn * kWaveN + j * 32 + frag_row][kk + frag_k]);
-#pragma unroll
-      for (int i = 0; i < kFragM; ++i)
-#pragma unroll
-        for (int j = 0; j < kFragN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < kFragM; ++i)
-#pragma unroll
-        for (int j = 0; j < kFragN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < kFragM; ++i)
-#pragma unroll
-        for (int j = 0; j < kFragN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < kFragM; ++i)
-#pragma unroll
-        for (int j = 0; j < kFragN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
+    for (int g = 0; g < kBK / 8; ++g) {
+      if (g + 1 < kBK / 8) load_frags((g + 1) & 1, buf, (g + 1) * 8);
+      mfma_group(g & 1);
     }
-    if (kt + 1 < nk) lds_store(buf ^ 1);
+    if (more) lds_store(buf ^ 1);
     __syncthreads();
+    if (more) load_frags(0, buf ^ 1, 0);
   }
 
   // Epilogue: lanes 0-31 and 32-63 each write 32 consecutive floats of a row.
