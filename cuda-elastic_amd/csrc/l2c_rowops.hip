@@ -8,7 +8,12 @@
 //    shuffles plus one LDS slot per wave, and writes the result from the same
 //    registers. HBM traffic is the floor: one read and one write per element
 //    (the reference's rmsnorm reads twice, its softmax reads 3x and writes 2x;
-//    llama2c/llama2c_cuda_graph.cu:58-115).
+//    llama2c/llama2c_cuda_graph.cu:58-115). When the lanes cover the row
+//    exactly (size 16384: 256 lanes x 16 float4) the loads and stores carry
+//    no bounds checks.
+//  * softmax needs one block barrier: each wavefront exponentiates against
+//    its own maximum (exp on the hardware exp2 with Cody-Waite reduction), and
+//    the waves' (max, sum) pairs are combined once (l2c_rows.h).
 //  * Rows whose address is not 16-byte aligned (size % 4 != 0) keep the same
 //    one-pass structure with scalar loads; rows longer than 1024 lanes x 64
 //    floats take a two-pass path that re-reads the row.
@@ -19,13 +24,12 @@
 //  * The naive product keeps the reference's one-lane-per-row structure and
 //    its sequential column order (one fused multiply-add per column), so its
 //    result is bit-reproducible by a CPU fmaf chain.
-#include "l2c_common.h"
+#include "l2c_rows.h"
 #include "../../include/l2c.h"
 
 namespace {
 
-using l2c::block_max;
-using l2c::block_sum;
+using l2c::Row;
 
 constexpr int kMaxRowThreads = 1024;
 constexpr int kGenericThreads = 256;
@@ -34,212 +38,35 @@ constexpr int kGenericThreads = 256;
 constexpr int kFusedThreads = 256;
 
 // ---------------------------------------------------------------------------
-// Row loaders. Thread t of a T-thread block holds chunk c = t + i*T for
-// i < V: a float4 (VEC) or, for unaligned rows, four scalars at element
-// t + (4i+s)*T (s < 4). Missing elements read as `fill`.
+// Kernels. V == 0 selects the two-pass generic path; MAXT is the launch
+// bound (256 or 1024 lanes), so rows that fit 256 lanes get the full register
+// budget.
 
-template <int V, bool VEC>
-struct Row {
-  float4 x[V];
-
-  __device__ __forceinline__ void load(const float *row, int size, float fill) {
-    const int T = blockDim.x, t = threadIdx.x;
-    if constexpr (VEC) {
-      const float4 *row4 = reinterpret_cast<const float4 *>(row);
-      const int cols4 = size >> 2;
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const int c = t + i * T;
-        x[i] = c < cols4 ? row4[c] : make_float4(fill, fill, fill, fill);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const int j0 = t + (4 * i) * T;
-        x[i].x = j0 < size ? row[j0] : fill;
-        x[i].y = j0 + T < size ? row[j0 + T] : fill;
-        x[i].z = j0 + 2 * T < size ? row[j0 + 2 * T] : fill;
-        x[i].w = j0 + 3 * T < size ? row[j0 + 3 * T] : fill;
-      }
-    }
-  }
-
-  // Stores x * scale * weight[j] (weight may be null: x * scale) for every
-  // valid element j, with 16-byte stores on the vector path.
-  __device__ __forceinline__ void store_scaled(float *row, int size, float scale,
-                                               const float *weight) const {
-    const int T = blockDim.x, t = threadIdx.x;
-    if constexpr (VEC) {
-      float4 *row4 = reinterpret_cast<float4 *>(row);
-      const float4 *w4 = reinterpret_cast<const float4 *>(weight);
-      const int cols4 = size >> 2;
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const int c = t + i * T;
-        if (c < cols4) {
-          float4 r;
-          if (weight != nullptr) {
-            const float4 g = w4[c];
-            r.x = x[i].x * scale * g.x;
-            r.y = x[i].y * scale * g.y;
-            r.z = x[i].z * scale * g.z;
-            r.w = x[i].w * scale * g.w;
-          } else {
-            r.x = x[i].x * scale;
-            r.y = x[i].y * scale;
-            r.z = x[i].z * scale;
-            r.w = x[i].w * scale;
-          }
-          l2c::st4_stream(row4 + c, r);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float v[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int j = t + (4 * i + s) * T;
-          if (j < size) row[j] = weight != nullptr ? v[s] * scale * weight[j] : v[s] * scale;
-        }
-      }
-    }
-  }
-};
-
-// ---------------------------------------------------------------------------
-// One row of each operation, executed by a whole block. `slots` is LDS
-// scratch with room for two reductions (2 x 16 floats).
-
-template <int V, bool VEC>
-__device__ __forceinline__ void rmsnorm_row(float *out, const float *in, const float *weight,
-                                            int size, float eps, float *slots) {
-  Row<V, VEC> r;
-  r.load(in, size, 0.0f);
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < V; ++i) {
-    ss = fmaf(r.x[i].x, r.x[i].x, ss);
-    ss = fmaf(r.x[i].y, r.x[i].y, ss);
-    ss = fmaf(r.x[i].z, r.x[i].z, ss);
-    ss = fmaf(r.x[i].w, r.x[i].w, ss);
-  }
-  ss = block_sum(ss, slots);
-  const float scale = 1.0f / sqrtf(ss / static_cast<float>(size) + eps);
-  r.store_scaled(out, size, scale, weight);
-}
-
-template <int V, bool VEC>
-__device__ __forceinline__ void softmax_row(float *out, const float *logits, int size,
-                                            float *slots) {
-  Row<V, VEC> r;
-  r.load(logits, size, -FLT_MAX);
-  float m = -FLT_MAX;
-#pragma unroll
-  for (int i = 0; i < V; ++i)
-    m = fmaxf(m, fmaxf(fmaxf(r.x[i].x, r.x[i].y), fmaxf(r.x[i].z, r.x[i].w)));
-  m = block_max(m, slots);
-  // exp of the padding (-FLT_MAX - m) underflows to exactly 0, so padding
-  // adds nothing to the sum.
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < V; ++i) {
-    r.x[i].x = expf(r.x[i].x - m);
-    r.x[i].y = expf(r.x[i].y - m);
-    r.x[i].z = expf(r.x[i].z - m);
-    r.x[i].w = expf(r.x[i].w - m);
-    s += (r.x[i].x + r.x[i].y) + (r.x[i].z + r.x[i].w);
-  }
-  s = block_sum(s, slots + 16);
-  const float inv = 1.0f / s;
-  r.store_scaled(out, size, inv, nullptr);
-}
-
-// Dot product of one matrix row with x, by a whole block (fused kernel). The
-// matrix row is loaded first (all V loads in flight), x is read per chunk.
-template <int V, bool VEC>
-__device__ __forceinline__ void matvec_row_block(float *out_elem, const float *mrow,
-                                                 const float *x, int size, float *slots) {
-  Row<V, VEC> w;
-  w.load(mrow, size, 0.0f);
-  const int T = blockDim.x, t = threadIdx.x;
-  float acc = 0.0f;
-#pragma unroll
-  for (int i = 0; i < V; ++i) {
-    float4 v;
-    if constexpr (VEC) {
-      const int c = t + i * T;
-      v = c < (size >> 2) ? reinterpret_cast<const float4 *>(x)[c] : make_float4(0, 0, 0, 0);
-    } else {
-      const int j0 = t + (4 * i) * T;
-      v.x = j0 < size ? x[j0] : 0.0f;
-      v.y = j0 + T < size ? x[j0 + T] : 0.0f;
-      v.z = j0 + 2 * T < size ? x[j0 + 2 * T] : 0.0f;
-      v.w = j0 + 3 * T < size ? x[j0 + 3 * T] : 0.0f;
-    }
-    acc = fmaf(w.x[i].x, v.x, acc);
-    acc = fmaf(w.x[i].y, v.y, acc);
-    acc = fmaf(w.x[i].z, v.z, acc);
-    acc = fmaf(w.x[i].w, v.w, acc);
-  }
-  acc = block_sum(acc, slots);
-  if (threadIdx.x == 0) *out_elem = acc;
-}
-
-// Two-pass versions for rows longer than the register-resident limit.
-__device__ void rmsnorm_row_generic(float *out, const float *in, const float *weight, int size,
-                                    float eps, float *slots) {
-  float ss = 0.0f;
-  for (int j = threadIdx.x; j < size; j += blockDim.x) ss = fmaf(in[j], in[j], ss);
-  ss = block_sum(ss, slots);
-  const float scale = 1.0f / sqrtf(ss / static_cast<float>(size) + eps);
-  for (int j = threadIdx.x; j < size; j += blockDim.x) out[j] = in[j] * scale * weight[j];
-}
-
-__device__ void softmax_row_generic(float *out, const float *logits, int size, float *slots) {
-  float m = -FLT_MAX;
-  for (int j = threadIdx.x; j < size; j += blockDim.x) m = fmaxf(m, logits[j]);
-  m = block_max(m, slots);
-  float s = 0.0f;
-  for (int j = threadIdx.x; j < size; j += blockDim.x) s += expf(logits[j] - m);
-  s = block_sum(s, slots + 16);
-  const float inv = 1.0f / s;
-  // Separate loops so the kernel is also correct in place (out == logits).
-  for (int j = threadIdx.x; j < size; j += blockDim.x) out[j] = expf(logits[j] - m) * inv;
-}
-
-__device__ void matvec_row_block_generic(float *out_elem, const float *mrow, const float *x,
-                                         int size, float *slots) {
-  float acc = 0.0f;
-  for (int j = threadIdx.x; j < size; j += blockDim.x) acc = fmaf(mrow[j], x[j], acc);
-  acc = block_sum(acc, slots);
-  if (threadIdx.x == 0) *out_elem = acc;
-}
-
-// ---------------------------------------------------------------------------
-// Kernels. V == 0 selects the two-pass generic path.
-
-template <int V, bool VEC>
-__global__ __launch_bounds__(kMaxRowThreads) void rmsnorm_kernel(float *out, const float *in,
-                                                                 const float *weight, int size,
-                                                                 float eps) {
+template <int V, bool VEC, bool EXACT, int MAXT>
+__global__ __launch_bounds__(MAXT) void rmsnorm_kernel(float *out, const float *in,
+                                                       const float *weight, int size, float eps) {
   __shared__ float slots[32];
   const size_t off = static_cast<size_t>(blockIdx.x) * size;
-  if constexpr (V == 0)
-    rmsnorm_row_generic(out + off, in + off, weight, size, eps, slots);
-  else
-    rmsnorm_row<V, VEC>(out + off, in + off, weight, size, eps, slots);
+  if constexpr (V == 0) {
+    l2c::rmsnorm_row_generic(out + off, in + off, weight, size, eps, slots);
+  } else {
+    Row<V, VEC, EXACT> r;
+    r.load(in + off, size, 0.0f);
+    l2c::rmsnorm_apply(r, out + off, weight, size, eps, slots);
+  }
 }
 
-template <int V, bool VEC>
-__global__ __launch_bounds__(kMaxRowThreads) void softmax_kernel(float *out, const float *logits,
-                                                                 int size) {
+template <int V, bool VEC, bool EXACT, int MAXT>
+__global__ __launch_bounds__(MAXT) void softmax_kernel(float *out, const float *logits, int size) {
   __shared__ float slots[32];
   const size_t off = static_cast<size_t>(blockIdx.x) * size;
-  if constexpr (V == 0)
-    softmax_row_generic(out + off, logits + off, size, slots);
-  else
-    softmax_row<V, VEC>(out + off, logits + off, size, slots);
+  if constexpr (V == 0) {
+    l2c::softmax_row_generic(out + off, logits + off, size, slots);
+  } else {
+    Row<V, VEC, EXACT> r;
+    r.load(logits + off, size, -FLT_MAX);
+    l2c::softmax_apply_1r(r, out + off, size, slots);
+  }
 }
 
 // One launch for a whole llama2c iteration. Block b handles:
@@ -247,8 +74,8 @@ __global__ __launch_bounds__(kMaxRowThreads) void softmax_kernel(float *out, con
 //   then                  the remaining rmsnorm rows, then remaining softmax rows
 //   then                  matrix-vector rows
 // so the short matrix-vector blocks fill the tail of the launch.
-template <int V, bool VEC>
-__global__ __launch_bounds__(kFusedThreads) void fused_kernel(
+template <int V, bool VEC, bool EXACT, int MAXT>
+__global__ __launch_bounds__(MAXT) void fused_kernel(
     float *normalized, const float *input, const float *weight, float *softmax,
     const float *logits, float *product, const float *matrix, int size, int rms_rows,
     int softmax_rows, float eps) {
@@ -271,13 +98,21 @@ __global__ __launch_bounds__(kFusedThreads) void fused_kernel(
   }
   const size_t off = static_cast<size_t>(row) * size;
   if constexpr (V == 0) {
-    if (kind == 0) rmsnorm_row_generic(normalized + off, input + off, weight, size, eps, slots);
-    else if (kind == 1) softmax_row_generic(softmax + off, logits + off, size, slots);
-    else matvec_row_block_generic(product + row, matrix + off, input, size, slots);
+    if (kind == 0) l2c::rmsnorm_row_generic(normalized + off, input + off, weight, size, eps, slots);
+    else if (kind == 1) l2c::softmax_row_generic(softmax + off, logits + off, size, slots);
+    else l2c::matvec_row_block_generic(product + row, matrix + off, input, size, slots);
   } else {
-    if (kind == 0) rmsnorm_row<V, VEC>(normalized + off, input + off, weight, size, eps, slots);
-    else if (kind == 1) softmax_row<V, VEC>(softmax + off, logits + off, size, slots);
-    else matvec_row_block<V, VEC>(product + row, matrix + off, input, size, slots);
+    if (kind == 0) {
+      Row<V, VEC, EXACT> r;
+      r.load(input + off, size, 0.0f);
+      l2c::rmsnorm_apply(r, normalized + off, weight, size, eps, slots);
+    } else if (kind == 1) {
+      Row<V, VEC, EXACT> r;
+      r.load(logits + off, size, -FLT_MAX);
+      l2c::softmax_apply_1r(r, softmax + off, size, slots);
+    } else {
+      l2c::matvec_row_block<V, VEC, EXACT>(product + row, matrix + off, input, size, slots);
+    }
   }
 }
 
@@ -349,11 +184,13 @@ __global__ __launch_bounds__(kMatvecWaves * L2C_WAVE) void matvec_wave_kernel(
 // ---------------------------------------------------------------------------
 // Launch configuration for the row kernels: the smallest V (float4 per lane)
 // whose row fits in <= 256 lanes, else in <= 1024 lanes, else the generic
-// two-pass path. Lanes are rounded up to whole wavefronts.
+// two-pass path. Lanes are rounded up to whole wavefronts; `exact` when the
+// lanes cover the row with no remainder.
 
 struct RowConfig {
   int threads;
   int v;  // 0 = generic
+  bool exact;
 };
 
 RowConfig choose_row_config(int size, int max_threads = kMaxRowThreads) {
@@ -363,10 +200,10 @@ RowConfig choose_row_config(int size, int max_threads = kMaxRowThreads) {
     for (int v = 1; v <= 16; v *= 2) {
       const int lanes = (chunks + v - 1) / v;
       const int threads = (lanes + L2C_WAVE - 1) / L2C_WAVE * L2C_WAVE;
-      if (threads <= limit) return {threads, v};
+      if (threads <= limit) return {threads, v, size % 4 == 0 && threads * v * 4 == size};
     }
   }
-  return {kGenericThreads, 0};
+  return {kGenericThreads, 0, false};
 }
 
 using RmsFn = void (*)(float *, const float *, const float *, int, float);
@@ -374,46 +211,69 @@ using SoftFn = void (*)(float *, const float *, int);
 using FusedFn = void (*)(float *, const float *, const float *, float *, const float *, float *,
                          const float *, int, int, int, float);
 
-int v_index(int v) {
+// Kernel instance for (V, vector path, exact, launch bound).
+template <int V, int MAXT>
+struct Pick {
+  static RmsFn rms(bool vec, bool exact) {
+    if (!vec) return rmsnorm_kernel<V, false, false, MAXT>;
+    return exact ? rmsnorm_kernel<V, true, true, MAXT> : rmsnorm_kernel<V, true, false, MAXT>;
+  }
+  static SoftFn soft(bool vec, bool exact) {
+    if (!vec) return softmax_kernel<V, false, false, MAXT>;
+    return exact ? softmax_kernel<V, true, true, MAXT> : softmax_kernel<V, true, false, MAXT>;
+  }
+  static FusedFn fused(bool vec, bool exact) {
+    if (!vec) return fused_kernel<V, false, false, MAXT>;
+    return exact ? fused_kernel<V, true, true, MAXT> : fused_kernel<V, true, false, MAXT>;
+  }
+};
+
+template <int MAXT>
+RmsFn rms_for(int v, bool vec, bool exact) {
   switch (v) {
-    case 1: return 1;
-    case 2: return 2;
-    case 4: return 3;
-    case 8: return 4;
-    case 16: return 5;
-    default: return 0;
+    case 1: return Pick<1, MAXT>::rms(vec, exact);
+    case 2: return Pick<2, MAXT>::rms(vec, exact);
+    case 4: return Pick<4, MAXT>::rms(vec, exact);
+    case 8: return Pick<8, MAXT>::rms(vec, exact);
+    case 16: return Pick<16, MAXT>::rms(vec, exact);
+    default: return rmsnorm_kernel<0, false, false, MAXT>;
   }
 }
 
-RmsFn rms_fn(int v, bool vec) {
-  static const RmsFn fv[] = {rmsnorm_kernel<0, false>, rmsnorm_kernel<1, true>,
-                             rmsnorm_kernel<2, true>,  rmsnorm_kernel<4, true>,
-                             rmsnorm_kernel<8, true>,  rmsnorm_kernel<16, true>};
-  static const RmsFn fs[] = {rmsnorm_kernel<0, false>, rmsnorm_kernel<1, false>,
-                             rmsnorm_kernel<2, false>, rmsnorm_kernel<4, false>,
-                             rmsnorm_kernel<8, false>, rmsnorm_kernel<16, false>};
-  return vec ? fv[v_index(v)] : fs[v_index(v)];
+template <int MAXT>
+SoftFn soft_for(int v, bool vec, bool exact) {
+  switch (v) {
+    case 1: return Pick<1, MAXT>::soft(vec, exact);
+    case 2: return Pick<2, MAXT>::soft(vec, exact);
+    case 4: return Pick<4, MAXT>::soft(vec, exact);
+    case 8: return Pick<8, MAXT>::soft(vec, exact);
+    case 16: return Pick<16, MAXT>::soft(vec, exact);
+    default: return softmax_kernel<0, false, false, MAXT>;
+  }
 }
 
-SoftFn soft_fn(int v, bool vec) {
-  static const SoftFn fv[] = {softmax_kernel<0, false>, softmax_kernel<1, true>,
-                              softmax_kernel<2, true>,  softmax_kernel<4, true>,
-                              softmax_kernel<8, true>,  softmax_kernel<16, true>};
-  static const SoftFn fs[] = {softmax_kernel<0, false>, softmax_kernel<1, false>,
-                              softmax_kernel<2, false>, softmax_kernel<4, false>,
-                              softmax_kernel<8, false>, softmax_kernel<16, false>};
-  return vec ? fv[v_index(v)] : fs[v_index(v)];
+FusedFn fused_for(int v, bool vec, bool exact) {
+  switch (v) {
+    case 1: return Pick<1, kFusedThreads>::fused(vec, exact);
+    case 2: return Pick<2, kFusedThreads>::fused(vec, exact);
+    case 4: return Pick<4, kFusedThreads>::fused(vec, exact);
+    case 8: return Pick<8, kFusedThreads>::fused(vec, exact);
+    case 16: return Pick<16, kFusedThreads>::fused(vec, exact);
+    default: return fused_kernel<0, false, false, kFusedThreads>;
+  }
 }
 
-FusedFn fused_fn(int v, bool vec) {
-  static const FusedFn fv[] = {fused_kernel<0, false>, fused_kernel<1, true>,
-                               fused_kernel<2, true>,  fused_kernel<4, true>,
-                               fused_kernel<8, true>,  fused_kernel<16, true>};
-  static const FusedFn fs[] = {fused_kernel<0, false>, fused_kernel<1, false>,
-                               fused_kernel<2, false>, fused_kernel<4, false>,
-                               fused_kernel<8, false>, fused_kernel<16, false>};
-  return vec ? fv[v_index(v)] : fs[v_index(v)];
+RmsFn rms_fn(const RowConfig &c, bool vec) {
+  const bool exact = vec && c.exact;
+  return c.threads <= 256 ? rms_for<256>(c.v, vec, exact) : rms_for<kMaxRowThreads>(c.v, vec, exact);
 }
+
+SoftFn soft_fn(const RowConfig &c, bool vec) {
+  const bool exact = vec && c.exact;
+  return c.threads <= 256 ? soft_for<256>(c.v, vec, exact) : soft_for<kMaxRowThreads>(c.v, vec, exact);
+}
+
+FusedFn fused_fn(const RowConfig &c, bool vec) { return fused_for(c.v, vec, vec && c.exact); }
 
 }  // namespace
 
@@ -428,7 +288,7 @@ extern "C" int l2c_rmsnorm(float *out, const float *in, const float *weight, int
   const RowConfig cfg = choose_row_config(size);
   const bool vec = size % 4 == 0 && l2c_aligned16(out) && l2c_aligned16(in) &&
                    l2c_aligned16(weight);
-  hipLaunchKernelGGL(rms_fn(cfg.v, vec), dim3(batch), dim3(cfg.threads), 0, stream, out, in,
+  hipLaunchKernelGGL(rms_fn(cfg, vec), dim3(batch), dim3(cfg.threads), 0, stream, out, in,
                      weight, size, eps);
   L2C_LAUNCH_CHECK();
   return hipSuccess;
@@ -441,7 +301,7 @@ extern "C" int l2c_softmax(float *out, const float *logits, int size, int batch,
   if (!out || !logits) return hipErrorInvalidValue;
   const RowConfig cfg = choose_row_config(size);
   const bool vec = size % 4 == 0 && l2c_aligned16(out) && l2c_aligned16(logits);
-  hipLaunchKernelGGL(soft_fn(cfg.v, vec), dim3(batch), dim3(cfg.threads), 0, stream, out, logits,
+  hipLaunchKernelGGL(soft_fn(cfg, vec), dim3(batch), dim3(cfg.threads), 0, stream, out, logits,
                      size);
   L2C_LAUNCH_CHECK();
   return hipSuccess;
@@ -485,7 +345,7 @@ extern "C" int l2c_fused(float *normalized, const float *input, const float *wei
   auto ok = [](const void *p) { return p == nullptr || l2c_aligned16(p); };
   const bool vec = size % 4 == 0 && ok(normalized) && ok(input) && ok(weight) && ok(softmax) &&
                    ok(logits) && ok(matrix);
-  hipLaunchKernelGGL(fused_fn(cfg.v, vec), dim3(static_cast<unsigned>(items)), dim3(cfg.threads),
+  hipLaunchKernelGGL(fused_fn(cfg, vec), dim3(static_cast<unsigned>(items)), dim3(cfg.threads),
                      0, stream, normalized, input, weight, softmax, logits, product, matrix, size,
                      rms_rows, softmax_rows, eps);
   L2C_LAUNCH_CHECK();
@@ -508,8 +368,8 @@ extern "C" int l2c_launch_shape(int op, int batch, int cols, int rows, int varia
     case L2C_OP_SOFTMAX: {
       const RowConfig cfg = choose_row_config(cols);
       const bool vec = cols % 4 == 0;
-      fn = op == L2C_OP_RMSNORM ? reinterpret_cast<const void *>(rms_fn(cfg.v, vec))
-                                : reinterpret_cast<const void *>(soft_fn(cfg.v, vec));
+      fn = op == L2C_OP_RMSNORM ? reinterpret_cast<const void *>(rms_fn(cfg, vec))
+                                : reinterpret_cast<const void *>(soft_fn(cfg, vec));
       *grid = batch;
       *block = cfg.threads;
       break;
@@ -530,7 +390,7 @@ extern "C" int l2c_launch_shape(int op, int batch, int cols, int rows, int varia
       break;
     case L2C_OP_FUSED: {
       const RowConfig cfg = choose_row_config(cols, kFusedThreads);
-      fn = reinterpret_cast<const void *>(fused_fn(cfg.v, cols % 4 == 0));
+      fn = reinterpret_cast<const void *>(fused_fn(cfg, cols % 4 == 0));
       *grid = 2 * batch + rows;
       *block = cfg.threads;
       break;

@@ -1,0 +1,276 @@
+// Device code of the row operations (rmsnorm, softmax, one matrix row dotted
+// with x), shared by the row kernels, the fused kernel and their tuning runs.
+//
+// A T-lane workgroup holds a row in VGPRs: lane t owns chunk c = t + i*T for
+// i < V, a float4 (VEC) or, for rows that are not 16-byte aligned, four
+// scalars at elements t + (4i + s)*T. EXACT means T * V * 4 == size, so no
+// lane needs a bounds check.
+#pragma once
+
+#include "l2c_common.h"
+
+namespace l2c {
+
+template <int V, bool VEC, bool EXACT>
+struct Row {
+  float4 x[V];
+
+  __device__ __forceinline__ void load(const float *row, int size, float fill) {
+    const int T = blockDim.x, t = threadIdx.x;
+    if constexpr (VEC) {
+      const float4 *row4 = reinterpret_cast<const float4 *>(row);
+      const int cols4 = size >> 2;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const int c = t + i * T;
+        if constexpr (EXACT) x[i] = row4[c];
+        else x[i] = c < cols4 ? row4[c] : make_float4(fill, fill, fill, fill);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const int j0 = t + (4 * i) * T;
+        x[i].x = j0 < size ? row[j0] : fill;
+        x[i].y = j0 + T < size ? row[j0 + T] : fill;
+        x[i].z = j0 + 2 * T < size ? row[j0 + 2 * T] : fill;
+        x[i].w = j0 + 3 * T < size ? row[j0 + 3 * T] : fill;
+      }
+    }
+  }
+
+  // Stores x * scale * weight[j] (weight may be null: x * scale) for every
+  // valid element j, with 16-byte nontemporal stores on the vector path.
+  __device__ __forceinline__ void store_scaled(float *row, int size, float scale,
+                                               const float *weight) const {
+    const int T = blockDim.x, t = threadIdx.x;
+    if constexpr (VEC) {
+      float4 *row4 = reinterpret_cast<float4 *>(row);
+      const float4 *w4 = reinterpret_cast<const float4 *>(weight);
+      const int cols4 = size >> 2;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const int c = t + i * T;
+        if (EXACT || c < cols4) {
+          float4 r;
+          if (weight != nullptr) {
+            const float4 g = w4[c];
+            r.x = x[i].x * scale * g.x;
+            r.y = x[i].y * scale * g.y;
+            r.z = x[i].z * scale * g.z;
+            r.w = x[i].w * scale * g.w;
+          } else {
+            r.x = x[i].x * scale;
+            r.y = x[i].y * scale;
+            r.z = x[i].z * scale;
+            r.w = x[i].w * scale;
+          }
+          st4_stream(row4 + c, r);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float v[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int j = t + (4 * i + s) * T;
+          if (j < size) row[j] = weight != nullptr ? v[s] * scale * weight[j] : v[s] * scale;
+        }
+      }
+    }
+  }
+};
+
+// Row reductions and transforms on a loaded row. `slots` is LDS scratch for
+// two block reductions (32 floats).
+
+template <int V, bool VEC, bool EXACT>
+__device__ __forceinline__ void rmsnorm_apply(Row<V, VEC, EXACT> &r, float *out, const float *weight,
+                                              int size, float eps, float *slots) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    ss = fmaf(r.x[i].x, r.x[i].x, ss);
+    ss = fmaf(r.x[i].y, r.x[i].y, ss);
+    ss = fmaf(r.x[i].z, r.x[i].z, ss);
+    ss = fmaf(r.x[i].w, r.x[i].w, ss);
+  }
+  ss = block_sum(ss, slots);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(size) + eps);
+  r.store_scaled(out, size, scale, weight);
+}
+
+// exp(t) for t <= 0 (softmax arguments x - max) on the hardware exp2
+// (v_exp_f32), with Cody-Waite range reduction (W. J. Cody and W. Waite,
+// Software Manual for the Elementary Functions, 1980): t = n ln2 + r with
+// n = rint(t / ln2) and |r| <= ln2 / 2, r computed with a two-part ln2
+// (16 + 24 bits) by fused multiply-adds, then exp(t) = 2^n * 2^(r / ln2).
+// The argument of v_exp_f32 is within [-1/2, 1/2], so its rounding
+// (2^-25 absolute) adds at most 1.8e-8 relative error to v_exp_f32's own
+// (about 1 ulp); the result is exact scaling by 2^n (v_ldexp_f32). Arguments
+// below -104 (results under the smallest float subnormal, including the
+// -FLT_MAX padding of a partial row) return 0; NaN propagates.
+__device__ __forceinline__ float exp_nonpositive(float t) {
+  constexpr float kLog2e = 1.44269504088896340736f;
+  constexpr float kLn2Hi = 0.693145751953125f;        // 16 significant bits
+  constexpr float kLn2Lo = 1.42860682030941723212e-6f; // ln2 - kLn2Hi
+  const float n = rintf(t * kLog2e);
+  float r = fmaf(-n, kLn2Hi, t);
+  r = fmaf(-n, kLn2Lo, r);
+  const float e = ldexpf(__builtin_amdgcn_exp2f(r * kLog2e), static_cast<int>(n));
+  return t < -104.0f ? 0.0f : e;
+}
+
+template <int V, bool VEC, bool EXACT, bool FAST_EXP = false>
+__device__ __forceinline__ void softmax_apply(Row<V, VEC, EXACT> &r, float *out, int size,
+                                              float *slots) {
+  float m = -FLT_MAX;
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+    m = fmaxf(m, fmaxf(fmaxf(r.x[i].x, r.x[i].y), fmaxf(r.x[i].z, r.x[i].w)));
+  m = block_max(m, slots);
+  // exp of padding (-FLT_MAX - m) underflows to exactly 0.
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    if constexpr (FAST_EXP) {
+      r.x[i].x = exp_nonpositive(r.x[i].x - m);
+      r.x[i].y = exp_nonpositive(r.x[i].y - m);
+      r.x[i].z = exp_nonpositive(r.x[i].z - m);
+      r.x[i].w = exp_nonpositive(r.x[i].w - m);
+    } else {
+      r.x[i].x = expf(r.x[i].x - m);
+      r.x[i].y = expf(r.x[i].y - m);
+      r.x[i].z = expf(r.x[i].z - m);
+      r.x[i].w = expf(r.x[i].w - m);
+    }
+    s += (r.x[i].x + r.x[i].y) + (r.x[i].z + r.x[i].w);
+  }
+  s = block_sum(s, slots + 16);
+  const float inv = 1.0f / s;
+  r.store_scaled(out, size, inv, nullptr);
+}
+
+// softmax with a single block reduction: each wavefront exponentiates
+// against its own maximum m_w and sums (s_w); the waves' (m_w, s_w) pairs
+// meet once in LDS, every lane combines them in wave order into the row
+// maximum M and S = sum_w s_w exp(m_w - M), and stores e * (exp(m_w - M) / S).
+// One barrier per row instead of two; one extra rounding per element.
+template <int V, bool VEC, bool EXACT>
+__device__ __forceinline__ void softmax_apply_1r(Row<V, VEC, EXACT> &r, float *out, int size,
+                                                 float *slots) {
+  float m = -FLT_MAX;
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+    m = fmaxf(m, fmaxf(fmaxf(r.x[i].x, r.x[i].y), fmaxf(r.x[i].z, r.x[i].w)));
+  m = wave_max(m);
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    r.x[i].x = exp_nonpositive(r.x[i].x - m);
+    r.x[i].y = exp_nonpositive(r.x[i].y - m);
+    r.x[i].z = exp_nonpositive(r.x[i].z - m);
+    r.x[i].w = exp_nonpositive(r.x[i].w - m);
+    s += (r.x[i].x + r.x[i].y) + (r.x[i].z + r.x[i].w);
+  }
+  s = wave_sum(s);
+  const int waves = blockDim.x / L2C_WAVE, w = threadIdx.x / L2C_WAVE;
+  if (threadIdx.x % L2C_WAVE == 0) {
+    slots[2 * w] = m;
+    slots[2 * w + 1] = s;
+  }
+  __syncthreads();
+  float M = -FLT_MAX;
+  for (int k = 0; k < waves; ++k) M = fmaxf(M, slots[2 * k]);
+  float S = 0.0f;
+  for (int k = 0; k < waves; ++k) S += slots[2 * k + 1] * exp_nonpositive(slots[2 * k] - M);
+  r.store_scaled(out, size, exp_nonpositive(m - M) / S, nullptr);
+}
+
+// Dot product of one matrix row with x by a whole block: the matrix row is
+// loaded first (all V loads in flight), x is read per chunk.
+template <int V, bool VEC, bool EXACT>
+__device__ __forceinline__ void matvec_row_block(float *out_elem, const float *mrow,
+                                                 const float *x, int size, float *slots) {
+  Row<V, VEC, EXACT> w;
+  w.load(mrow, size, 0.0f);
+  const int T = blockDim.x, t = threadIdx.x;
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    float4 v;
+    if constexpr (VEC) {
+      const int c = t + i * T;
+      if constexpr (EXACT) v = reinterpret_cast<const float4 *>(x)[c];
+      else v = c < (size >> 2) ? reinterpret_cast<const float4 *>(x)[c] : make_float4(0, 0, 0, 0);
+    } else {
+      const int j0 = t + (4 * i) * T;
+      v.x = j0 < size ? x[j0] : 0.0f;
+      v.y = j0 + T < size ? x[j0 + T] : 0.0f;
+      v.z = j0 + 2 * T < size ? x[j0 + 2 * T] : 0.0f;
+      v.w = j0 + 3 * T < size ? x[j0 + 3 * T] : 0.0f;
+    }
+    acc = fmaf(w.x[i].x, v.x, acc);
+    acc = fmaf(w.x[i].y, v.y, acc);
+    acc = fmaf(w.x[i].z, v.z, acc);
+    acc = fmaf(w.x[i].w, v.w, acc);
+  }
+  acc = block_sum(acc, slots);
+  if (threadIdx.x == 0) *out_elem = acc;
+}
+
+// Two-pass versions for rows longer than the register-resident limit.
+__device__ inline void rmsnorm_row_generic(float *out, const float *in, const float *weight,
+                                           int size, float eps, float *slots) {
+  float ss = 0.0f;
+  for (int j = threadIdx.x; j < size; j += blockDim.x) ss = fmaf(in[j], in[j], ss);
+  ss = block_sum(ss, slots);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(size) + eps);
+  for (int j = threadIdx.x; j < size; j += blockDim.x) out[j] = in[j] * scale * weight[j];
+}
+
+__device__ inline void softmax_row_generic(float *out, const float *logits, int size,
+                                           float *slots) {
+  float m = -FLT_MAX;
+  for (int j = threadIdx.x; j < size; j += blockDim.x) m = fmaxf(m, logits[j]);
+  m = block_max(m, slots);
+  float s = 0.0f;
+  for (int j = threadIdx.x; j < size; j += blockDim.x) s += expf(logits[j] - m);
+  s = block_sum(s, slots + 16);
+  const float inv = 1.0f / s;
+  // Separate loops so the kernel is also correct in place (out == logits).
+  for (int j = threadIdx.x; j < size; j += blockDim.x) out[j] = expf(logits[j] - m) * inv;
+}
+
+__device__ inline void matvec_row_block_generic(float *out_elem, const float *mrow,
+                                                const float *x, int size, float *slots) {
+  float acc = 0.0f;
+  for (int j = threadIdx.x; j < size; j += blockDim.x) acc = fmaf(mrow[j], x[j], acc);
+  acc = block_sum(acc, slots);
+  if (threadIdx.x == 0) *out_elem = acc;
+}
+
+// Row loop shared by the rmsnorm and softmax kernels: block b handles rows
+// b, b + G, b + 2G, ... (G = gridDim.x). The next row's loads are issued
+// before the current row is reduced and stored, so one block keeps HBM busy
+// through its reductions. LDS slot sets alternate between rows: a set is
+// rewritten only after every lane has passed the next row's barrier.
+template <int V, bool VEC, bool EXACT, typename Apply>
+__device__ __forceinline__ void row_loop(const float *in, float *out, int size, int batch,
+                                         float fill, float *slots, Apply apply) {
+  int row = blockIdx.x;
+  if (row >= batch) return;
+  Row<V, VEC, EXACT> cur;
+  cur.load(in + static_cast<size_t>(row) * size, size, fill);
+  for (int parity = 0;; parity ^= 1) {
+    const int next = row + static_cast<int>(gridDim.x);
+    Row<V, VEC, EXACT> nxt;
+    if (next < batch) nxt.load(in + static_cast<size_t>(next) * size, size, fill);
+    apply(cur, out + static_cast<size_t>(row) * size, slots + 32 * parity);
+    if (next >= batch) break;
+    cur = nxt;
+    row = next;
+  }
+}
+
+}  // namespace l2c
