@@ -143,6 +143,9 @@ def main():
             ("c3_direct_nocopy", cfg("direct", 10000, 8, 768, 2048, "nocopy", "coalesced", warm=100)),
             ("c3_graph_copy", cfg("graph", 10000, 8, 768, 2048, "copy", "coalesced", warm=100)),
             ("c3_direct_copy", cfg("direct", 10000, 8, 768, 2048, "copy", "coalesced", warm=100)),
+            ("c3_fused_graph_nocopy", cfg("graph", 10000, 8, 768, 2048, "nocopy", "fused", warm=100)),
+            ("c3_fused_direct_nocopy", cfg("direct", 10000, 8, 768, 2048, "nocopy", "fused", warm=100)),
+            ("c3_fused_direct_copy", cfg("direct", 10000, 8, 768, 2048, "copy", "fused", warm=100)),
             ("c5_mxfp4_graph_nocopy", cfg("graph", K, B, S, R, "nocopy", "mxfp4", inputs="normal=1")),
             ("c5_fp8_graph_nocopy", cfg("graph", K, B, S, R, "nocopy", "fp8", inputs="normal=1")),
         ]
