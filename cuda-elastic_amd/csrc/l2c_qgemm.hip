@@ -6,15 +6,26 @@
 //  * The activations are bf16 and must stay bf16 (the oracle multiplies the
 //    exact bf16 values), so the product runs on the bf16 matrix cores
 //    (v_mfma_f32_32x32x16_bf16, fp32 accumulation).
-//  * Weights are dequantized exactly to bf16 on their way into LDS, once per
-//    workgroup and k-step: an e2m1 magnitude times a power of two, or an e4m3
-//    value, has at most 4 significant bits, so the bf16 value is exact. The
-//    fp8 row scale is applied once per output in the epilogue.
-//  * Tile 256 (batch) x 128 (rows) x 64 (k), 8 wavefronts of 64 x 64, double-
-//    buffered LDS with a 144-byte row stride (conflict-free 16-byte fragment
-//    reads). MFMA operand layout: lane l supplies A[l % 32][8 * (l / 32) + 0..7]
-//    and B[8 * (l / 32) + 0..7][l % 32]; the accumulator layout matches the
-//    fp32 kernel's.
+//  * Weights are converted exactly to bf16 in registers by the gfx950 scaled
+//    conversions (v_cvt_scalef32_pk_bf16_fp4 / _fp8: two codes to two bf16,
+//    times the block scale 2^(s - 127)): an e2m1 magnitude times a power of
+//    two, or an e4m3 value, has at most 4 significant bits, so the bf16 value
+//    is exact. The fp8 row scale is applied once per output in the epilogue.
+//  * Tile 256 (batch) x 128 (rows) x 64 (k), 8 wavefronts of 64 x 64 (2 x 2
+//    blocks of 32 x 32). Only the activations use LDS: a double-buffered slab
+//    with a 144-byte row stride (conflict-free 16-byte fragment reads). W never
+//    touches LDS: each wavefront loads the codes of its own 64 rows from
+//    global memory (L2) into registers and converts them into MFMA B operands.
+//  * Two steps of prefetch: the X slab and the W codes of step t + 2 are
+//    loaded while step t multiplies, so the 0.5 us of MFMA work per step does
+//    not wait for L2 latency. Register sets alternate with the step's parity.
+//  * k permutation: within a step, lane (r, h) (r = lane % 32, h = lane / 32)
+//    of MFMA q in 0..3 supplies k = 32h + 8q + j (j < 8) for both operands, so
+//    a lane's W codes for the step are 32 consecutive k (16 contiguous bytes of
+//    MXFP4) and its X fragment of MFMA q is 8 contiguous bf16 in LDS. MFMA
+//    operand layout: lane l supplies A[l % 32][8 * (l / 32) + 0..7] and
+//    B[8 * (l / 32) + 0..7][l % 32]; the accumulator layout matches the fp32
+//    kernel's.
 //  * Workgroup order is remapped per XCD as in the fp32 kernel.
 //
 // Encodings (bit-identical to the host encoders of the harness):
@@ -23,6 +34,8 @@
 //    even k in the low nibble. Block of 32 k: e8m0 scale 2^(s - 127) with
 //    s - 127 = floor(log2(amax / 6)) clamped to [-127, 127].
 //  * e4m3 (OCP, bias 7, max 448, no infinities): nearest-even, saturating.
+#include <type_traits>
+
 #include "l2c_common.h"
 #include "../../include/l2c.h"
 
@@ -30,6 +43,7 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 256;
 constexpr int kBN = 128;
@@ -45,12 +59,9 @@ constexpr int kStride = kBK + 8;  // bf16 per LDS row (144 bytes)
 constexpr int kXChunks = kBM * (kBK / 8) / kThreads;  // 16-byte X chunks per thread: 4
 constexpr int kXcds = 8;
 
-static_assert(kBN * (kBK / 16) == kThreads, "one 16-element weight chunk per thread");
+constexpr int kSteps = kBK / 16;  // MFMAs per 32 x 32 block and k-step (4)
 
-struct Smem {
-  uint16_t a[2][kBM][kStride];
-  uint16_t b[2][kBN][kStride];
-};
+static_assert(kBK == 64, "the k permutation gives each lane half 32 consecutive k per step");
 
 // ---------------------------------------------------------------------------
 // Element encoders / decoders.
@@ -100,24 +111,6 @@ __device__ __forceinline__ int mxfp4_exponent(float amax) {
 
 __device__ __forceinline__ float pow2f(int e) {  // e in [-126, 127]
   return __uint_as_float(static_cast<unsigned>(e + 127) << 23);
-}
-
-// bf16 bits of an e2m1 code times 2^x (exact: at most 2 significant bits).
-__device__ __forceinline__ uint16_t e2m1_to_bf16(unsigned code, float scale) {
-  constexpr float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
-  float v = mag[code & 7u] * scale;
-  if (code & 8u) v = -v;
-  return static_cast<uint16_t>(__float_as_uint(v) >> 16);
-}
-
-// bf16 bits of an e4m3 code (exact).
-__device__ __forceinline__ uint16_t e4m3_to_bf16(unsigned code) {
-  const unsigned e = (code >> 3) & 15u, m = code & 7u;
-  unsigned bits;
-  if (e == 0) bits = __float_as_uint(static_cast<float>(m) * 0.001953125f);  // m * 2^-9
-  else bits = ((e + 120u) << 23) | (m << 20);
-  bits |= (code & 0x80u) << 24;
-  return static_cast<uint16_t>(bits >> 16);
 }
 
 // ---------------------------------------------------------------------------
@@ -182,7 +175,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
                                                          const uint8_t *__restrict__ Wq,
                                                          const void *__restrict__ scales,
                                                          int M, int N, int K) {
-  __shared__ Smem sm;
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kBM][kStride];
   int tile = blockIdx.x;
   const int tiles = gridDim.x;
   if (tiles % kXcds == 0) tile = (tile % kXcds) * (tiles / kXcds) + tile / kXcds;
@@ -195,72 +188,98 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
   const int wave = t / L2C_WAVE;
   const int wm = wave % kWavesM;
   const int wn = wave / kWavesM;
+  const int r = lane % 32;
+  const int h = lane / 32;
+  const int nk = (K + kBK - 1) / kBK;
 
-  // This thread's weight chunk: 16 consecutive k of one row.
-  const int wrow = t / (kBK / 16);
-  const int wchunk = t % (kBK / 16);
-  const int wr = n0 + wrow;
-
-  uint4 gx[kXChunks];
-  uint4 gw;        // raw codes: 8 bytes (mxfp4, in .x/.y) or 16 bytes (fp8)
-  unsigned gs = 0; // mxfp4 scale byte
-
-  auto global_load = [&](int k0) {
+  // X slab. Loads are clamped into the operand and used as loaded: rows past
+  // M only feed outputs that are never stored, and k past K meets W codes
+  // zeroed when the B operand is formed (finite x times 0 is 0).
+  u32x4 gx[2][kXChunks];
+  auto x_load = [&](u32x4 (&g)[kXChunks], int k0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kXChunks; ++i) {
       const int idx = t + i * kThreads;
       const int row = m0 + idx / (kBK / 8);
       const int k = k0 + (idx % (kBK / 8)) * 8;
-      gx[i] = (row < M && k < K)
-                  ? *reinterpret_cast<const uint4 *>(X + static_cast<size_t>(row) * K + k)
-                  : make_uint4(0, 0, 0, 0);
-    }
-    const int k = k0 + wchunk * 16;
-    const bool ok = wr < N && k < K;
-    if constexpr (FMT == L2C_Q_MXFP4) {
-      if (ok) {
-        const uint2 c = *reinterpret_cast<const uint2 *>(Wq + static_cast<size_t>(wr) * (K / 2) + k / 2);
-        gw = make_uint4(c.x, c.y, 0, 0);
-        gs = static_cast<const uint8_t *>(scales)[static_cast<size_t>(wr) * (K / 32) + k / 32];
-      } else {
-        gw = make_uint4(0, 0, 0, 0);
-        gs = 127;
-      }
-    } else {
-      gw = ok ? *reinterpret_cast<const uint4 *>(Wq + static_cast<size_t>(wr) * K + k)
-              : make_uint4(0, 0, 0, 0);
+      g[i] = *reinterpret_cast<const u32x4 *>(
+          X + static_cast<size_t>(row < M ? row : M - 1) * K + (k < K ? k : K - 8));
     }
   };
-
-  auto lds_store = [&](int buf) {
+  auto x_store = [&](const u32x4 (&g)[kXChunks], int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kXChunks; ++i) {
       const int idx = t + i * kThreads;
-      *reinterpret_cast<uint4 *>(&sm.a[buf][idx / (kBK / 8)][(idx % (kBK / 8)) * 8]) = gx[i];
+      *reinterpret_cast<u32x4 *>(&xs[buf][idx / (kBK / 8)][(idx % (kBK / 8)) * 8]) = g[i];
     }
-    uint32_t h[8];  // 16 bf16, two per word
+  };
+
+  // This lane's W row in each 32-row block and its codes for one step.
+  int wrow[kFragN];
+#pragma unroll
+  for (int j = 0; j < kFragN; ++j) {
+    const int n = n0 + wn * kWaveN + j * 32 + r;
+    wrow[j] = n < N ? n : N - 1;
+  }
+  // Raw codes are kept exactly as loaded (no arithmetic on a load result
+  // until it is used two steps later, so the loads stay in flight); rows past
+  // N read a clamped row whose outputs are never stored, and k past K is
+  // zeroed when the operand is formed.
+  constexpr int kWords = FMT == L2C_Q_MXFP4 ? 4 : 8;  // dwords of codes per block and step
+  uint32_t raw[2][kFragN][kWords];
+  uint32_t sraw[2][kFragN];  // MXFP4 scale bytes as loaded
+  bool kin[2];               // this lane half's k range lies inside K
+  auto w_load = [&](uint32_t (&rw)[kFragN][kWords], uint32_t (&sr)[kFragN], bool &kok,
+                    int k0) __attribute__((always_inline)) {
+    const int k = k0 + 32 * h;
+    kok = k < K;
+    const int kc = kok ? k : K - 32;
+#pragma unroll
+    for (int j = 0; j < kFragN; ++j) {
+      if constexpr (FMT == L2C_Q_MXFP4) {
+        const uint4 v =
+            *reinterpret_cast<const uint4 *>(Wq + static_cast<size_t>(wrow[j]) * (K / 2) + kc / 2);
+        rw[j][0] = v.x;
+        rw[j][1] = v.y;
+        rw[j][2] = v.z;
+        rw[j][3] = v.w;
+        sr[j] = static_cast<const uint8_t *>(scales)[static_cast<size_t>(wrow[j]) * (K / 32) + kc / 32];
+      } else {
+        const uint4 *p = reinterpret_cast<const uint4 *>(Wq + static_cast<size_t>(wrow[j]) * K + kc);
+        const uint4 v0 = p[0], v1 = p[1];
+        rw[j][0] = v0.x;
+        rw[j][1] = v0.y;
+        rw[j][2] = v0.z;
+        rw[j][3] = v0.w;
+        rw[j][4] = v1.x;
+        rw[j][5] = v1.y;
+        rw[j][6] = v1.z;
+        rw[j][7] = v1.w;
+      }
+    }
+  };
+  // B operand of MFMA q for block j: W[k = 32h + 8q + 0..7] of row wrow[j].
+  auto w_operand = [&](const uint32_t (&rw)[kFragN][kWords], const uint32_t (&sr)[kFragN],
+                       bool kok, int j, int q) __attribute__((always_inline)) {
+    uint32_t d[4];
     if constexpr (FMT == L2C_Q_MXFP4) {
-      // 2^(gs - 127); gs = 0 is the subnormal 2^-127.
-      const float scale = gs == 0 ? __uint_as_float(0x00400000u) : pow2f(static_cast<int>(gs) - 127);
-      const uint32_t words[2] = {gw.x, gw.y};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t w = words[i / 4];
-        const unsigned lo = (w >> (8 * (i % 4))) & 15u, hi = (w >> (8 * (i % 4) + 4)) & 15u;
-        h[i] = e2m1_to_bf16(lo, scale) | (static_cast<uint32_t>(e2m1_to_bf16(hi, scale)) << 16);
-      }
+      // Block scale 2^(s - 127) as fp32 (s = 0 is the subnormal 2^-127); 0
+      // outside K, which zeroes the converted values.
+      const uint32_t sc = sr[j] & 0xffu;
+      const float scale = __uint_as_float(kok ? (sc == 0 ? 0x00400000u : (sc << 23)) : 0u);
+      const uint32_t w = rw[j][q];  // codes k = 8q .. 8q + 7, two per byte
+      d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0));
+      d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1));
+      d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2));
+      d[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3));
     } else {
-      const uint32_t words[4] = {gw.x, gw.y, gw.z, gw.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t w = words[i / 2];
-        const unsigned lo = (w >> (16 * (i % 2))) & 0xffu, hi = (w >> (16 * (i % 2) + 8)) & 0xffu;
-        h[i] = e4m3_to_bf16(lo) | (static_cast<uint32_t>(e4m3_to_bf16(hi)) << 16);
-      }
+      const uint32_t w0 = kok ? rw[j][2 * q] : 0u, w1 = kok ? rw[j][2 * q + 1] : 0u;
+      d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false));
+      d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true));
+      d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false));
+      d[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true));
     }
-    uint4 *dst = reinterpret_cast<uint4 *>(&sm.b[buf][wrow][wchunk * 16]);
-    dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
-    dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
+    return __builtin_bit_cast(bf16x8, make_uint4(d[0], d[1], d[2], d[3]));
   };
 
   f32x16 acc[kFragM][kFragN];
@@ -271,45 +290,60 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  const int frag_row = lane % 32;
-  const int frag_k = 8 * (lane / 32);
-  const int nk = (K + kBK - 1) / kBK;
+  const uint16_t *a_base = &xs[0][wm * kWaveM + r][32 * h];
+  constexpr int kBuf = kBM * kStride;
 
-  global_load(0);
-  lds_store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) global_load((kt + 1) * kBK);
+  // One k-step; its parity P names its LDS buffer and register sets.
+  auto step = [&](auto parity, int kt) __attribute__((always_inline)) {
+    constexpr int P = decltype(parity)::value;
+    bf16x8 bop[kFragN][kSteps];
 #pragma unroll
-    for (int kk = 0; kk < kBK; kk += 16) {
-      bf16x8 a[kFragM], b[kFragN];
+    for (int j = 0; j < kFragN; ++j)
+#pragma unroll
+      for (int q = 0; q < kSteps; ++q) bop[j][q] = w_operand(raw[P], sraw[P], kin[P], j, q);
+    if (kt + 2 < nk) {  // step t + 2 into the registers just consumed
+      x_load(gx[P], (kt + 2) * kBK);
+      w_load(raw[P], sraw[P], kin[P], (kt + 2) * kBK);
+    }
+#pragma unroll
+    for (int q = 0; q < kSteps; ++q) {
+      bf16x8 a[kFragM];
 #pragma unroll
       for (int i = 0; i < kFragM; ++i)
-        a[i] = *reinterpret_cast<const bf16x8 *>(&sm.a[buf][wm * kWaveM + i * 32 + frag_row][kk + frag_k]);
-#pragma unroll
-      for (int j = 0; j < kFragN; ++j)
-        b[j] = *reinterpret_cast<const bf16x8 *>(&sm.b[buf][wn * kWaveN + j * 32 + frag_row][kk + frag_k]);
+        a[i] = *reinterpret_cast<const bf16x8 *>(a_base + P * kBuf + i * 32 * kStride + 8 * q);
 #pragma unroll
       for (int i = 0; i < kFragM; ++i)
 #pragma unroll
         for (int j = 0; j < kFragN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bop[j][q], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nk) lds_store(buf ^ 1);
+    if (kt + 1 < nk) x_store(gx[P ^ 1], P ^ 1);  // the slab of step t + 1
     __syncthreads();
+  };
+
+  x_load(gx[0], 0);
+  w_load(raw[0], sraw[0], kin[0], 0);
+  if (nk > 1) {
+    x_load(gx[1], kBK);
+    w_load(raw[1], sraw[1], kin[1], kBK);
+  }
+  x_store(gx[0], 0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(std::integral_constant<int, 0>(), kt);
+    if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
   }
 
 #pragma unroll
   for (int j = 0; j < kFragN; ++j) {
-    const int n = n0 + wn * kWaveN + j * 32 + lane % 32;
+    const int n = n0 + wn * kWaveN + j * 32 + r;
     float rs = 1.0f;
     if constexpr (FMT == L2C_Q_FP8) rs = n < N ? static_cast<const float *>(scales)[n] : 0.0f;
 #pragma unroll
     for (int i = 0; i < kFragM; ++i) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int m = m0 + wm * kWaveM + i * 32 + 8 * (v / 4) + 4 * (lane / 32) + v % 4;
+        const int m = m0 + wm * kWaveM + i * 32 + 8 * (v / 4) + 4 * h + v % 4;
         if (m < M && n < N) out[static_cast<size_t>(m) * N + n] = acc[i][j][v] * rs;
       }
     }
