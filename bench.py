@@ -107,8 +107,11 @@ def cpu_baseline(batch, size, rows, sample_vectors, sample_rows_norm):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    # 100 warm-up iterations (~0.2 s at the headline shape): the matrix cores
+    # need about that long under load to reach their steady clock, and the
+    # reference's own default warm-up is 100 ms (llama2c_cuda_graph.cu:43-53).
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--quick", action="store_true", help="headline and cpu baseline only")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()

@@ -61,6 +61,16 @@ __device__ __forceinline__ void st4_stream(float4 *p, float4 v) {
   __builtin_nontemporal_store(w, reinterpret_cast<f32x4 *>(p));
 }
 
+// Raw buffer resource over [p, p + bytes). Loads through it take a 32-bit
+// per-lane byte offset plus a wave-uniform byte offset held in a scalar
+// register, so a loop that walks along K advances one SGPR per step and
+// spends no vector instructions on addresses. Word 3 selects the 32-bit data
+// format that untyped (raw) buffer loads require on gfx9-family parts.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
 }  // namespace l2c
 
 // Return code plumbing shared by the extern "C" entry points.

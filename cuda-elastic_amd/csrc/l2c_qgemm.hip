@@ -12,13 +12,22 @@
 //    two, or an e4m3 value, has at most 4 significant bits, so the bf16 value
 //    is exact. The fp8 row scale is applied once per output in the epilogue.
 //  * Tile 256 (batch) x 128 (rows) x 64 (k), 8 wavefronts of 64 x 64 (2 x 2
-//    blocks of 32 x 32). Only the activations use LDS: a double-buffered slab
-//    with a 144-byte row stride (conflict-free 16-byte fragment reads). W never
-//    touches LDS: each wavefront loads the codes of its own 64 rows from
-//    global memory (L2) into registers and converts them into MFMA B operands.
-//  * Two steps of prefetch: the X slab and the W codes of step t + 2 are
-//    loaded while step t multiplies, so the 0.5 us of MFMA work per step does
-//    not wait for L2 latency. Register sets alternate with the step's parity.
+//    blocks of 32 x 32); 4 x 64 = 256 tiles at 1024 x 8192, one per CU.
+//  * Each k-step's X slab (256 rows x 128 B), W codes (128 rows x 32 or 64 B)
+//    and MXFP4 block scales (converted once to fp32 by the staging thread)
+//    pass through a three-stage LDS ring: step t multiplies stage t % 3,
+//    stores step t + 2 into stage (t + 2) % 3, and reads step t + 1's
+//    fragments into registers before the step's barrier, so no wave waits on
+//    LDS latency after a barrier. Global loads run four steps ahead through
+//    two register sets. Every thread stages the same amount (branch-free).
+//  * Buffer loads: per-lane byte offsets are computed once (rows past the
+//    operand clamped) and the k-step is a scalar offset. A partial last step
+//    (K % 64 == 32) runs after the loop; its lanes past K read in-bounds
+//    codes and get zero B operands.
+//  * LDS layouts are bank-conflict free for both the staging stores and the
+//    fragment reads: X rows are padded to 144 B; W rows are unpadded with
+//    their 16-byte chunks XOR-swizzled by row bits; scales are a separate
+//    [128][2] fp32 array.
 //  * k permutation: within a step, lane (r, h) (r = lane % 32, h = lane / 32)
 //    of MFMA q in 0..3 supplies k = 32h + 8q + j (j < 8) for both operands, so
 //    a lane's W codes for the step are 32 consecutive k (16 contiguous bytes of
@@ -51,17 +60,32 @@ constexpr int kBK = 64;
 constexpr int kWavesM = 4;
 constexpr int kWavesN = 2;
 constexpr int kThreads = kWavesM * kWavesN * L2C_WAVE;  // 512
-constexpr int kWaveM = kBM / kWavesM;
-constexpr int kWaveN = kBN / kWavesN;
-constexpr int kFragM = kWaveM / 32;
-constexpr int kFragN = kWaveN / 32;
-constexpr int kStride = kBK + 8;  // bf16 per LDS row (144 bytes)
-constexpr int kXChunks = kBM * (kBK / 8) / kThreads;  // 16-byte X chunks per thread: 4
+constexpr int kFragM = kBM / kWavesM / 32;              // 2
+constexpr int kFragN = kBN / kWavesN / 32;              // 2
+constexpr int kStages = 3;
+constexpr int kXStride = 144;                           // LDS bytes per X row (64 bf16 + 16 pad)
+constexpr int kXChunks = kBM * (kBK / 8) / kThreads;    // 16-byte X chunks per thread and step: 4
 constexpr int kXcds = 8;
+// The X tile of one workgroup must stay addressable with 32-bit offsets.
+constexpr long long kMaxTileBytes = 0xffffffffLL;
 
-constexpr int kSteps = kBK / 16;  // MFMAs per 32 x 32 block and k-step (4)
-
-static_assert(kBK == 64, "the k permutation gives each lane half 32 consecutive k per step");
+// Per-format staging geometry. W rows hold the step's codes (32 bytes of
+// MXFP4 or 64 of fp8) with 16-byte chunks XOR-swizzled by row bits; MXFP4
+// block scales follow as fp32 [kBN][2].
+template <int FMT>
+struct Geometry {
+  static constexpr int kWRow = FMT == L2C_Q_MXFP4 ? 32 : 64;  // code bytes per W row and step
+  static constexpr int kWBytes = kWRow * kBN / kThreads;      // code bytes staged per thread
+  static constexpr int kWReads = FMT == L2C_Q_MXFP4 ? 1 : 2;  // 16-byte code reads per block
+  static constexpr int kXStage = kBM * kXStride;
+  static constexpr int kSStage = kXStage + kBN * kWRow;
+  static constexpr int kStage = kSStage + (FMT == L2C_Q_MXFP4 ? kBN * 8 : 0);
+  // Chunk swizzle: 16 lanes reading chunk c of 16 consecutive rows (or 32
+  // lanes storing 8 rows) touch 64 distinct banks.
+  static __device__ __forceinline__ int swizzle(int row) {
+    return FMT == L2C_Q_MXFP4 ? (row >> 3) & 1 : (row >> 2) & 3;
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Element encoders / decoders.
@@ -175,111 +199,76 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
                                                          const uint8_t *__restrict__ Wq,
                                                          const void *__restrict__ scales,
                                                          int M, int N, int K) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kBM][kStride];
+  using G = Geometry<FMT>;
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kStages * G::kStage];
+
   int tile = blockIdx.x;
   const int tiles = gridDim.x;
   if (tiles % kXcds == 0) tile = (tile % kXcds) * (tiles / kXcds) + tile / kXcds;
   const int mtiles = (M + kBM - 1) / kBM;
   const int m0 = (tile % mtiles) * kBM;
   const int n0 = (tile / mtiles) * kBN;
-
-  const int t = threadIdx.x;
-  const int lane = t % L2C_WAVE;
-  const int wave = t / L2C_WAVE;
+  const int mrows = min(kBM, M - m0), nrows = min(kBN, N - n0);
+  const int tid = threadIdx.x;
+  const int lane = tid % L2C_WAVE;
+  const int wave = tid / L2C_WAVE;
   const int wm = wave % kWavesM;
   const int wn = wave / kWavesM;
   const int r = lane % 32;
   const int h = lane / 32;
-  const int nk = (K + kBK - 1) / kBK;
 
-  // X slab. Loads are clamped into the operand and used as loaded: rows past
-  // M only feed outputs that are never stored, and k past K meets W codes
-  // zeroed when the B operand is formed (finite x times 0 is 0).
-  u32x4 gx[2][kXChunks];
-  auto x_load = [&](u32x4 (&g)[kXChunks], int k0) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < kXChunks; ++i) {
-      const int idx = t + i * kThreads;
-      const int row = m0 + idx / (kBK / 8);
-      const int k = k0 + (idx % (kBK / 8)) * 8;
-      g[i] = *reinterpret_cast<const u32x4 *>(
-          X + static_cast<size_t>(row < M ? row : M - 1) * K + (k < K ? k : K - 8));
-    }
-  };
-  auto x_store = [&](const u32x4 (&g)[kXChunks], int buf) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < kXChunks; ++i) {
-      const int idx = t + i * kThreads;
-      *reinterpret_cast<u32x4 *>(&xs[buf][idx / (kBK / 8)][(idx % (kBK / 8)) * 8]) = g[i];
-    }
-  };
+  const int wrow_bytes = FMT == L2C_Q_MXFP4 ? K / 2 : K;
+  const __amdgpu_buffer_rsrc_t rx =
+      l2c::buffer_rsrc(X + static_cast<size_t>(m0) * K, static_cast<uint32_t>(mrows) * K * 2u);
+  const __amdgpu_buffer_rsrc_t rw =
+      l2c::buffer_rsrc(Wq + static_cast<size_t>(n0) * wrow_bytes, static_cast<uint32_t>(nrows) * wrow_bytes);
+  const __amdgpu_buffer_rsrc_t rs = l2c::buffer_rsrc(
+      static_cast<const uint8_t *>(scales) + (FMT == L2C_Q_MXFP4 ? static_cast<size_t>(n0) * (K / 32) : 0),
+      FMT == L2C_Q_MXFP4 ? static_cast<uint32_t>(nrows) * (K / 32) : 4u);
 
-  // This lane's W row in each 32-row block and its codes for one step.
-  int wrow[kFragN];
+  // Staging assignments (global byte offsets without the step part, LDS
+  // offsets within a stage).
+  int xg[kXChunks], xs[kXChunks];
 #pragma unroll
-  for (int j = 0; j < kFragN; ++j) {
-    const int n = n0 + wn * kWaveN + j * 32 + r;
-    wrow[j] = n < N ? n : N - 1;
+  for (int v = 0; v < kXChunks; ++v) {
+    const int id = v * kThreads + tid, row = id / 8, c = id % 8;
+    xg[v] = min(row, mrows - 1) * K * 2 + 16 * c;
+    xs[v] = row * kXStride + 16 * c;
   }
-  // Raw codes are kept exactly as loaded (no arithmetic on a load result
-  // until it is used two steps later, so the loads stay in flight); rows past
-  // N read a clamped row whose outputs are never stored, and k past K is
-  // zeroed when the operand is formed.
-  constexpr int kWords = FMT == L2C_Q_MXFP4 ? 4 : 8;  // dwords of codes per block and step
-  uint32_t raw[2][kFragN][kWords];
-  uint32_t sraw[2][kFragN];  // MXFP4 scale bytes as loaded
-  bool kin[2];               // this lane half's k range lies inside K
-  auto w_load = [&](uint32_t (&rw)[kFragN][kWords], uint32_t (&sr)[kFragN], bool &kok,
-                    int k0) __attribute__((always_inline)) {
-    const int k = k0 + 32 * h;
-    kok = k < K;
-    const int kc = kok ? k : K - 32;
+  const int wrow = tid / (G::kWRow / G::kWBytes);
+  const int wbyte = G::kWBytes * (tid % (G::kWRow / G::kWBytes));
+  const int wg = min(wrow, nrows - 1) * wrow_bytes + wbyte;
+  const int ws = G::kXStage + wrow * G::kWRow + (((wbyte >> 4) ^ G::swizzle(wrow)) << 4) + (wbyte & 15);
+  // MXFP4 scales: threads t and t + 256 stage the same (row, half) word.
+  const int srow = (tid & 255) / 2, shalf = tid & 1;
+  const int sg = min(srow, nrows - 1) * (K / 32) + shalf;
+  const int ss = G::kSStage + (srow * 2 + shalf) * 4;
+
+  u32x4 gx[2][kXChunks];
+  u32x4 gw4[2];
+  u32x2 gw2[2];
+  uint32_t gs[2];
+  auto gload = [&](auto set, int t) __attribute__((always_inline)) {
+    constexpr int st = decltype(set)::value;
 #pragma unroll
-    for (int j = 0; j < kFragN; ++j) {
-      if constexpr (FMT == L2C_Q_MXFP4) {
-        const uint4 v =
-            *reinterpret_cast<const uint4 *>(Wq + static_cast<size_t>(wrow[j]) * (K / 2) + kc / 2);
-        rw[j][0] = v.x;
-        rw[j][1] = v.y;
-        rw[j][2] = v.z;
-        rw[j][3] = v.w;
-        sr[j] = static_cast<const uint8_t *>(scales)[static_cast<size_t>(wrow[j]) * (K / 32) + kc / 32];
-      } else {
-        const uint4 *p = reinterpret_cast<const uint4 *>(Wq + static_cast<size_t>(wrow[j]) * K + kc);
-        const uint4 v0 = p[0], v1 = p[1];
-        rw[j][0] = v0.x;
-        rw[j][1] = v0.y;
-        rw[j][2] = v0.z;
-        rw[j][3] = v0.w;
-        rw[j][4] = v1.x;
-        rw[j][5] = v1.y;
-        rw[j][6] = v1.z;
-        rw[j][7] = v1.w;
-      }
-    }
+    for (int v = 0; v < kXChunks; ++v) gx[st][v] = __builtin_amdgcn_raw_buffer_load_b128(rx, xg[v], 128 * t, 0);
+    if constexpr (G::kWBytes == 16) gw4[st] = __builtin_amdgcn_raw_buffer_load_b128(rw, wg, G::kWRow * t, 0);
+    else gw2[st] = __builtin_amdgcn_raw_buffer_load_b64(rw, wg, G::kWRow * t, 0);
+    if constexpr (FMT == L2C_Q_MXFP4) gs[st] = __builtin_amdgcn_raw_buffer_load_b8(rs, sg, 2 * t, 0);
   };
-  // B operand of MFMA q for block j: W[k = 32h + 8q + 0..7] of row wrow[j].
-  auto w_operand = [&](const uint32_t (&rw)[kFragN][kWords], const uint32_t (&sr)[kFragN],
-                       bool kok, int j, int q) __attribute__((always_inline)) {
-    uint32_t d[4];
+  auto lstore = [&](auto set, int stage) __attribute__((always_inline)) {
+    constexpr int st = decltype(set)::value;
+    unsigned char *base = lds + stage * G::kStage;
+#pragma unroll
+    for (int v = 0; v < kXChunks; ++v) *reinterpret_cast<u32x4 *>(base + xs[v]) = gx[st][v];
+    if constexpr (G::kWBytes == 16) *reinterpret_cast<u32x4 *>(base + ws) = gw4[st];
+    else *reinterpret_cast<u32x2 *>(base + ws) = gw2[st];
     if constexpr (FMT == L2C_Q_MXFP4) {
-      // Block scale 2^(s - 127) as fp32 (s = 0 is the subnormal 2^-127); 0
-      // outside K, which zeroes the converted values.
-      const uint32_t sc = sr[j] & 0xffu;
-      const float scale = __uint_as_float(kok ? (sc == 0 ? 0x00400000u : (sc << 23)) : 0u);
-      const uint32_t w = rw[j][q];  // codes k = 8q .. 8q + 7, two per byte
-      d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0));
-      d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1));
-      d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2));
-      d[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3));
-    } else {
-      const uint32_t w0 = kok ? rw[j][2 * q] : 0u, w1 = kok ? rw[j][2 * q + 1] : 0u;
-      d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false));
-      d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true));
-      d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false));
-      d[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true));
+      // Block scale 2^(s - 127) as fp32 (s = 0 is the subnormal 2^-127).
+      const uint32_t e = gs[st] & 0xffu;
+      *reinterpret_cast<uint32_t *>(base + ss) = e == 0 ? 0x00400000u : (e << 23);
     }
-    return __builtin_bit_cast(bf16x8, make_uint4(d[0], d[1], d[2], d[3]));
   };
 
   f32x16 acc[kFragM][kFragN];
@@ -290,61 +279,137 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  const uint16_t *a_base = &xs[0][wm * kWaveM + r][32 * h];
-  constexpr int kBuf = kBM * kStride;
-
-  // One k-step; its parity P names its LDS buffer and register sets.
-  auto step = [&](auto parity, int kt) __attribute__((always_inline)) {
-    constexpr int P = decltype(parity)::value;
-    bf16x8 bop[kFragN][kSteps];
+  // This lane's fragments: X row wm * 64 + 32 i + r, W row brow + 32 j.
+  const int a_off = (wm * kFragM * 32 + r) * kXStride + 64 * h;
+  const int brow = wn * kFragN * 32 + r;
+  const int s_off = G::kSStage + (brow * 2 + h) * 4;
+  struct Frags {
+    u32x4 w[kFragN][G::kWReads];
+    uint32_t s[kFragN];
+    u32x4 a[kFragM][4];
+  };
+  auto read_frags = [&](int stage, Frags &f) __attribute__((always_inline)) {
+    const unsigned char *base = lds + stage * G::kStage;
 #pragma unroll
-    for (int j = 0; j < kFragN; ++j)
+    for (int j = 0; j < kFragN; ++j) {
 #pragma unroll
-      for (int q = 0; q < kSteps; ++q) bop[j][q] = w_operand(raw[P], sraw[P], kin[P], j, q);
-    if (kt + 2 < nk) {  // step t + 2 into the registers just consumed
-      x_load(gx[P], (kt + 2) * kBK);
-      w_load(raw[P], sraw[P], kin[P], (kt + 2) * kBK);
+      for (int v = 0; v < G::kWReads; ++v) {
+        const int row = brow + 32 * j;
+        const int chunk = (FMT == L2C_Q_MXFP4 ? h : 2 * h + v) ^ G::swizzle(row);
+        f.w[j][v] = *reinterpret_cast<const u32x4 *>(base + G::kXStage + row * G::kWRow + 16 * chunk);
+      }
+      if constexpr (FMT == L2C_Q_MXFP4)
+        f.s[j] = *reinterpret_cast<const uint32_t *>(base + s_off + j * 32 * 8);
     }
 #pragma unroll
-    for (int q = 0; q < kSteps; ++q) {
-      bf16x8 a[kFragM];
+    for (int q = 0; q < 4; ++q)
 #pragma unroll
       for (int i = 0; i < kFragM; ++i)
-        a[i] = *reinterpret_cast<const bf16x8 *>(a_base + P * kBuf + i * 32 * kStride + 8 * q);
+        f.a[i][q] = *reinterpret_cast<const u32x4 *>(base + a_off + i * 32 * kXStride + 16 * q);
+  };
+  // B operand of MFMA q for block j: W[k = 32h + 8q + 0..7] of row brow + 32 j;
+  // zero when kok is false (lanes past K in the partial last step).
+  auto mma = [&](const Frags &f, bool kok) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bf16x8 b[kFragN];
+#pragma unroll
+      for (int j = 0; j < kFragN; ++j) {
+        uint32_t d[4];
+        if constexpr (FMT == L2C_Q_MXFP4) {
+          const float scale = __uint_as_float(kok ? f.s[j] : 0u);
+          const uint32_t c = f.w[j][0][q];  // codes k = 8q .. 8q + 7, two per byte
+          d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 0));
+          d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 1));
+          d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 2));
+          d[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 3));
+        } else {
+          const uint32_t c0 = kok ? f.w[j][q / 2][2 * (q % 2)] : 0u;
+          const uint32_t c1 = kok ? f.w[j][q / 2][2 * (q % 2) + 1] : 0u;
+          d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c0, 1.0f, false));
+          d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c0, 1.0f, true));
+          d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c1, 1.0f, false));
+          d[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c1, 1.0f, true));
+        }
+        b[j] = __builtin_bit_cast(bf16x8, make_uint4(d[0], d[1], d[2], d[3]));
+      }
 #pragma unroll
       for (int i = 0; i < kFragM; ++i)
 #pragma unroll
         for (int j = 0; j < kFragN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bop[j][q], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, f.a[i][q]), b[j],
+                                                              acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nk) x_store(gx[P ^ 1], P ^ 1);  // the slab of step t + 1
-    __syncthreads();
   };
 
-  x_load(gx[0], 0);
-  w_load(raw[0], sraw[0], kin[0], 0);
-  if (nk > 1) {
-    x_load(gx[1], kBK);
-    w_load(raw[1], sraw[1], kin[1], kBK);
+  Frags fr[2];
+  const int nfull = K / kBK;
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  if (nfull > 0) {
+    // Steps past the last are clamped to it: redundant in-bounds loads whose
+    // copies are never read.
+    const int last = nfull - 1;
+    gload(I0(), 0);
+    gload(I1(), min(1, last));
+    lstore(I0(), 0);
+    gload(I0(), min(2, last));
+    lstore(I1(), 1);
+    gload(I1(), min(3, last));
+    __syncthreads();
+    read_frags(0, fr[0]);
+    int rd = 0;  // stage of the current step
+    int t = 0;
+    auto step = [&](auto set) __attribute__((always_inline)) {
+      constexpr int st = decltype(set)::value;
+      const int nx = rd == kStages - 1 ? 0 : rd + 1;
+      const int wr = rd == 0 ? kStages - 1 : rd - 1;
+      read_frags(nx, fr[st ^ 1]);
+      mma(fr[st], true);
+      lstore(set, wr);
+      gload(set, min(t + 4, last));
+      __syncthreads();
+      rd = nx;
+      ++t;
+    };
+    for (; t + 2 <= nfull;) {
+      step(I0());
+      step(I1());
+    }
+    if (t < nfull) mma(fr[0], true);
   }
-  x_store(gx[0], 0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; kt += 2) {
-    step(std::integral_constant<int, 0>(), kt);
-    if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
+  if (K % kBK != 0) {
+    // Half step at k0 = 64 * nfull: chunks past K read in-bounds data from
+    // the valid half, and the B operands of lanes h = 1 are zero.
+    __syncthreads();
+    const int t2 = nfull;
+#pragma unroll
+    for (int v = 0; v < kXChunks; ++v) {
+      const int c = (v * kThreads + tid) % 8;
+      gx[0][v] = __builtin_amdgcn_raw_buffer_load_b128(rx, xg[v] - (c >= 4 ? 64 : 0), 128 * t2, 0);
+    }
+    const int half = G::kWRow / 2;
+    const int wgo = wg - (wbyte >= half ? half : 0);
+    if constexpr (G::kWBytes == 16) gw4[0] = __builtin_amdgcn_raw_buffer_load_b128(rw, wgo, G::kWRow * t2, 0);
+    else gw2[0] = __builtin_amdgcn_raw_buffer_load_b64(rw, wgo, G::kWRow * t2, 0);
+    if constexpr (FMT == L2C_Q_MXFP4) gs[0] = __builtin_amdgcn_raw_buffer_load_b8(rs, sg - shalf, 2 * t2, 0);
+    lstore(I0(), 0);
+    __syncthreads();
+    read_frags(0, fr[0]);
+    mma(fr[0], h == 0);
   }
 
 #pragma unroll
   for (int j = 0; j < kFragN; ++j) {
-    const int n = n0 + wn * kWaveN + j * 32 + r;
-    float rs = 1.0f;
-    if constexpr (FMT == L2C_Q_FP8) rs = n < N ? static_cast<const float *>(scales)[n] : 0.0f;
+    const int n = brow + 32 * j;
+    float rs_ = 1.0f;
+    if constexpr (FMT == L2C_Q_FP8) rs_ = n < nrows ? static_cast<const float *>(scales)[n0 + n] : 0.0f;
 #pragma unroll
     for (int i = 0; i < kFragM; ++i) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int m = m0 + wm * kWaveM + i * 32 + 8 * (v / 4) + 4 * h + v % 4;
-        if (m < M && n < N) out[static_cast<size_t>(m) * N + n] = acc[i][j][v] * rs;
+        const int m = wm * kFragM * 32 + 32 * i + 8 * (v / 4) + 4 * h + v % 4;
+        if (m < mrows && n < nrows) out[static_cast<size_t>(m0 + m) * N + n0 + n] = acc[i][j][v] * rs_;
       }
     }
   }
@@ -370,6 +435,7 @@ extern "C" int l2c_matmul_q(float *out, const void *Xbf16, const void *Wq, const
   if (batch == 0 || rows == 0) return hipSuccess;
   if (!out || !Xbf16 || !Wq || !scales) return hipErrorInvalidValue;
   if (!l2c_aligned16(Xbf16) || !l2c_aligned16(Wq)) return hipErrorInvalidValue;
+  if (static_cast<long long>(kBM) * cols * 2 > kMaxTileBytes) return hipErrorInvalidValue;
   const long long tiles =
       static_cast<long long>((batch + kBM - 1) / kBM) * ((rows + kBN - 1) / kBN);
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;

@@ -171,7 +171,8 @@ def test_fused_partial_items(torch_gpu, l2c, orc):
 
 @pytest.mark.parametrize("batch,size,rows", [(1, 288, 288), (8, 768, 2048), (64, 1000, 300),
                                              (33, 1001, 77), (256, 512, 128), (300, 96, 200),
-                                             (512, 2048, 1024), (2, 5, 3)])
+                                             (512, 2048, 1024), (2, 5, 3), (3, 20, 5),
+                                             (130, 4100, 257)])
 @pytest.mark.parametrize("mode", ["scaled", "deterministic", "random"])
 def test_matmul_batched(torch_gpu, l2c, orc, batch, size, rows, mode):
     torch = torch_gpu

@@ -67,7 +67,7 @@ def test_quantize_fp8_exact(torch_gpu, l2c, orc, rows, cols):
 
 @pytest.mark.parametrize("fmt", [0, 1])
 @pytest.mark.parametrize("batch,size,rows", [(8, 64, 16), (300, 1024, 200), (256, 4096, 256),
-                                             (33, 96, 77)])
+                                             (33, 96, 77), (5, 32, 9), (130, 2080, 140)])
 def test_matmul_q(torch_gpu, l2c, orc, fmt, batch, size, rows):
     torch = torch_gpu
     print(f"case matmul_q fmt={fmt} batch={batch} size={size} rows={rows}", flush=True)
