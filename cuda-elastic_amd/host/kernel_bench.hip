@@ -5,7 +5,7 @@
 // time and HBM bytes to a single kernel (llama2c/profile_cuda.sh:136-167
 // isolates kernels the same way with ncu).
 //
-//   l2c_kernel_bench OP BATCH SIZE ROWS ITERS
+//   l2c_kernel_bench OP BATCH SIZE ROWS ITERS   (after >= 100 ms of warm-up launches)
 //   OP: rmsnorm softmax gemv naive fused matmul mxfp4 fp8 copy
 //
 // `copy` runs a plain 16-byte-per-lane copy of BATCH x SIZE floats (read
@@ -145,11 +145,21 @@ int main(int argc, char **argv) {
       std::exit(2);
     }
   };
-  launch();  // warm-up
-  CHECK(hipStreamSynchronize(s));
   hipEvent_t t0, t1;
   CHECK(hipEventCreate(&t0));
   CHECK(hipEventCreate(&t1));
+  // Warm-up of 100 ms (at least 3 and at most 1000 launches): the matrix cores reach their
+  // steady clock only after some tens of milliseconds under load.
+  int warm = 0;
+  float warm_ms = 0.0f;
+  CHECK(hipEventRecord(t0, s));
+  while (warm < 3 || (warm_ms < 100.0f && warm < 1000)) {
+    launch();
+    ++warm;
+    CHECK(hipEventRecord(t1, s));
+    CHECK(hipEventSynchronize(t1));
+    CHECK(hipEventElapsedTime(&warm_ms, t0, t1));
+  }
   CHECK(hipEventRecord(t0, s));
   for (int i = 0; i < iters; ++i) launch();
   CHECK(hipEventRecord(t1, s));
@@ -157,7 +167,7 @@ int main(int argc, char **argv) {
   float ms = 0;
   CHECK(hipEventElapsedTime(&ms, t0, t1));
   const double us = 1000.0 * ms / iters;
-  std::printf("op=%s batch=%d size=%d rows=%d iters=%d avg_us=%.3f bytes=%.0f gbps=%.1f tflops=%.3f\n",
-              op.c_str(), B, S, R, iters, us, bytes, bytes / (us * 1e3), flops / (us * 1e6));
+  std::printf("op=%s batch=%d size=%d rows=%d iters=%d warmup=%d avg_us=%.3f bytes=%.0f gbps=%.1f tflops=%.3f\n",
+              op.c_str(), B, S, R, iters, warm, us, bytes, bytes / (us * 1e3), flops / (us * 1e6));
   return 0;
 }
