@@ -1,0 +1,229 @@
+// Device kernels of the batched greedy decoder (rmsnorm of each sequence's
+// current token -> dense classifier -> softmax + argmax with the argmax fed
+// back as the next token), the pipeline of
+// applications/loom_private/decoder/decoder.cu:200-367. The classifier itself
+// is l2c_matmul (gemm_f32_mfma_kernel); this file holds the model generator
+// and the two row kernels around it.
+//
+// Row kernels: one workgroup of 256 lanes per sequence, rows streamed with
+// 16-byte loads where the row is 16-byte aligned. Reductions are wave64
+// butterflies combined across the four waves in wave order, so every result
+// is deterministic (the decoder's check compares repeated invocations and
+// direct against graph launches bitwise).
+#include <climits>
+
+#include "l2c_common.h"
+#include "../../include/l2c.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / L2C_WAVE;
+
+// Synthetic model (decoder.cu:30-43): embedding row t is 1 except 4 at
+// column t; the norm weight is 1; classifier row r is 0 except 1 at column
+// (r + vocab - 1) mod vocab.
+__global__ void decoder_init_model_kernel(float *embedding, float *classifier, float *norm_weight,
+                                          int width, int vocab) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  const size_t first = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const size_t total = static_cast<size_t>(vocab) * width;
+  for (size_t i = first; i < total; i += stride) {
+    const int row = static_cast<int>(i / width);
+    const int column = static_cast<int>(i % width);
+    embedding[i] = column == row ? 4.0f : 1.0f;
+    classifier[i] = column == (row + vocab - 1) % vocab ? 1.0f : 0.0f;
+  }
+  for (size_t j = first; j < static_cast<size_t>(width); j += stride) norm_weight[j] = 1.0f;
+}
+
+// Sum over the workgroup: butterflies within each wave, then the four wave
+// totals in wave order. `slots` holds kWaves floats; callers alternate slot
+// sets between consecutive reductions.
+__device__ __forceinline__ float group_sum(float v, float *slots) {
+  v = l2c::wave_sum(v);
+  if (threadIdx.x % L2C_WAVE == 0) slots[threadIdx.x / L2C_WAVE] = v;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) total += slots[w];
+  return total;
+}
+
+__device__ __forceinline__ float group_max(float v, float *slots) {
+  v = l2c::wave_max(v);
+  if (threadIdx.x % L2C_WAVE == 0) slots[threadIdx.x / L2C_WAVE] = v;
+  __syncthreads();
+  float m = slots[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) m = fmaxf(m, slots[w]);
+  return m;
+}
+
+// llama2.c rmsnorm of the embedding row of each sequence's current token
+// (decoder.cu:45-77): ss = sum x^2; ss /= width; ss += 1e-5f;
+// scale = 1 / sqrtf(ss); o_j = w_j * (scale * x_j). An out-of-range token
+// (a corrupted state, or the poisoned token buffer) gives a NaN row, so the
+// check fails instead of reading outside the embedding.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void decoder_rmsnorm_kernel(float *normalized,
+                                                                   const int *tokens,
+                                                                   const float *embedding,
+                                                                   const float *weight, int width,
+                                                                   int vocab) {
+#pragma clang fp contract(off)  // separate multiply and add, as the contract's builds
+  __shared__ float slots[kWaves];
+  const int sequence = blockIdx.x;
+  const int token = tokens[sequence];
+  float *o = normalized + static_cast<size_t>(sequence) * width;
+  const int t = threadIdx.x;
+  if (token < 0 || token >= vocab) {
+    for (int j = t; j < width; j += kThreads) o[j] = __builtin_nanf("");
+    return;
+  }
+  const float *x = embedding + static_cast<size_t>(token) * width;
+  float ss = 0.0f;
+  if constexpr (VEC) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    for (int c = t; c < width / 4; c += kThreads) {
+      const float4 v = x4[c];
+      ss += v.x * v.x;
+      ss += v.y * v.y;
+      ss += v.z * v.z;
+      ss += v.w * v.w;
+    }
+  } else {
+    for (int j = t; j < width; j += kThreads) ss += x[j] * x[j];
+  }
+  ss = group_sum(ss, slots);
+  ss /= static_cast<float>(width);
+  ss += 1e-5f;
+  const float scale = 1.0f / sqrtf(ss);
+  if constexpr (VEC) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    const float4 *w4 = reinterpret_cast<const float4 *>(weight);
+    float4 *o4 = reinterpret_cast<float4 *>(o);
+    for (int c = t; c < width / 4; c += kThreads) {
+      const float4 v = x4[c], g = w4[c];
+      o4[c] = make_float4(g.x * (scale * v.x), g.y * (scale * v.y), g.z * (scale * v.z),
+                          g.w * (scale * v.w));
+    }
+  } else {
+    for (int j = t; j < width; j += kThreads) o[j] = weight[j] * (scale * x[j]);
+  }
+}
+
+// llama2.c softmax (max-subtracted expf divided by the float sum) followed by
+// sample_argmax (the first maximum of the probabilities), decoder.cu:127-198.
+// The argmax is the sequence's next token: written to tokens[sequence] for
+// the next step and recorded in generated[sequence][step]. No maximum (every
+// probability NaN) gives token -1.
+__global__ __launch_bounds__(kThreads) void decoder_softmax_argmax_kernel(
+    float *probabilities, const float *logits, int *tokens, int *generated, int vocab, int steps,
+    int step) {
+#pragma clang fp contract(off)
+  __shared__ float slots[3 * kWaves];
+  __shared__ int islots[kWaves];
+  const int sequence = blockIdx.x;
+  const float *x = logits + static_cast<size_t>(sequence) * vocab;
+  float *p = probabilities + static_cast<size_t>(sequence) * vocab;
+  const int t = threadIdx.x;
+
+  float maximum = -INFINITY;
+  for (int r = t; r < vocab; r += kThreads) maximum = fmaxf(maximum, x[r]);
+  maximum = group_max(maximum, slots);
+
+  float sum = 0.0f;
+  for (int r = t; r < vocab; r += kThreads) {
+    const float e = expf(x[r] - maximum);
+    p[r] = e;
+    sum += e;
+  }
+  sum = group_sum(sum, slots + kWaves);
+
+  // Each lane normalizes the entries it wrote (its own stores, visible to
+  // itself) and keeps the first maximum among them.
+  float best = -INFINITY;
+  int best_index = INT_MAX;
+  for (int r = t; r < vocab; r += kThreads) {
+    const float q = p[r] / sum;
+    p[r] = q;
+    if (q > best) {
+      best = q;
+      best_index = r;
+    }
+  }
+  // (value, index) maximum with ties to the smaller index: butterflies, then
+  // the waves in order.
+#pragma unroll
+  for (int offset = L2C_WAVE / 2; offset > 0; offset >>= 1) {
+    const float ov = __shfl_xor(best, offset, L2C_WAVE);
+    const int oi = __shfl_xor(best_index, offset, L2C_WAVE);
+    if (ov > best || (ov == best && oi < best_index)) {
+      best = ov;
+      best_index = oi;
+    }
+  }
+  float *vslots = slots + 2 * kWaves;
+  if (t % L2C_WAVE == 0) {
+    vslots[t / L2C_WAVE] = best;
+    islots[t / L2C_WAVE] = best_index;
+  }
+  __syncthreads();
+  if (t == 0) {
+    float v = vslots[0];
+    int i = islots[0];
+    for (int w = 1; w < kWaves; ++w) {
+      if (vslots[w] > v || (vslots[w] == v && islots[w] < i)) {
+        v = vslots[w];
+        i = islots[w];
+      }
+    }
+    const int next = i == INT_MAX ? -1 : i;
+    tokens[sequence] = next;
+    generated[static_cast<size_t>(sequence) * steps + step] = next;
+  }
+}
+
+}  // namespace
+
+extern "C" int l2c_decoder_init_model(float *embedding, float *classifier, float *norm_weight,
+                                      int width, int vocab, hipStream_t stream) {
+  if (width <= 0 || vocab <= 0) return hipErrorInvalidValue;
+  if (!embedding || !classifier || !norm_weight) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(decoder_init_model_kernel, dim3(4096), dim3(256), 0, stream, embedding,
+                     classifier, norm_weight, width, vocab);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+extern "C" int l2c_decoder_rmsnorm(float *normalized, const int *tokens, const float *embedding,
+                                   const float *weight, int width, int vocab, int batch,
+                                   hipStream_t stream) {
+  if (width <= 0 || vocab <= 0 || batch < 0) return hipErrorInvalidValue;
+  if (batch == 0) return hipSuccess;
+  if (!normalized || !tokens || !embedding || !weight) return hipErrorInvalidValue;
+  const bool vec = width % 4 == 0 && l2c_aligned16(normalized) && l2c_aligned16(embedding) &&
+                   l2c_aligned16(weight);
+  if (vec)
+    hipLaunchKernelGGL(decoder_rmsnorm_kernel<true>, dim3(batch), dim3(kThreads), 0, stream,
+                       normalized, tokens, embedding, weight, width, vocab);
+  else
+    hipLaunchKernelGGL(decoder_rmsnorm_kernel<false>, dim3(batch), dim3(kThreads), 0, stream,
+                       normalized, tokens, embedding, weight, width, vocab);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+extern "C" int l2c_decoder_softmax_argmax(float *probabilities, const float *logits, int *tokens,
+                                          int *generated, int vocab, int batch, int steps,
+                                          int step, hipStream_t stream) {
+  if (vocab <= 0 || batch < 0 || steps <= 0 || step < 0 || step >= steps)
+    return hipErrorInvalidValue;
+  if (batch == 0) return hipSuccess;
+  if (!probabilities || !logits || !tokens || !generated) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(decoder_softmax_argmax_kernel, dim3(batch), dim3(kThreads), 0, stream,
+                     probabilities, logits, tokens, generated, vocab, steps, step);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}

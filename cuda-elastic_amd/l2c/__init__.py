@@ -24,6 +24,7 @@ BIN_DIR = os.path.join(PKG_DIR, "bin")
 LIB_PATH = os.path.join(LIB_DIR, "libl2c.so")
 HOST_LIB_PATH = os.path.join(LIB_DIR, "libl2c_host.so")
 HARNESS = os.path.join(BIN_DIR, "llama2c_hip")
+DECODER = os.path.join(BIN_DIR, "llama2c_decoder_hip")
 COMPARE = os.path.join(BIN_DIR, "l2c_compare")
 
 RMS_EPSILON = 1.0e-5  # llama2c/llama2c_common.h:44
@@ -39,8 +40,9 @@ KERNEL_SYMBOLS = (
     "l2c_rmsnorm", "l2c_softmax", "l2c_matvec", "l2c_fused", "l2c_matmul", "l2c_matmul_q",
     "l2c_quantize_mxfp4", "l2c_quantize_fp8", "l2c_to_bf16", "l2c_launch_shape",
     "l2c_strerror", "l2c_version",
+    "l2c_decoder_init_model", "l2c_decoder_rmsnorm", "l2c_decoder_softmax_argmax",
 )
-HOST_SYMBOLS = ("l2c_harness_main", "l2c_compare_dumps")
+HOST_SYMBOLS = ("l2c_harness_main", "l2c_compare_dumps", "l2c_decoder_main", "l2c_decoder_run")
 
 
 class L2CError(RuntimeError):
@@ -85,6 +87,9 @@ def load() -> ctypes.CDLL:
         "l2c_quantize_fp8": [p, p, p, i, i, p],
         "l2c_to_bf16": [p, p, sz, p],
         "l2c_launch_shape": [i, i, i, i, i, ctypes.POINTER(i), ctypes.POINTER(i), ctypes.POINTER(i)],
+        "l2c_decoder_init_model": [p, p, p, i, i, p],
+        "l2c_decoder_rmsnorm": [p, p, p, p, i, i, i, p],
+        "l2c_decoder_softmax_argmax": [p, p, p, p, i, i, i, i, p],
     }
     for name, args in sigs.items():
         fn = getattr(lib, name)
@@ -112,6 +117,11 @@ def load_host() -> ctypes.CDLL:
     host.l2c_harness_main.restype = ctypes.c_int
     host.l2c_compare_dumps.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_char_p)]
     host.l2c_compare_dumps.restype = ctypes.c_int
+    host.l2c_decoder_main.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_char_p), ctypes.c_char_p,
+                                      ctypes.c_size_t]
+    host.l2c_decoder_main.restype = ctypes.c_int
+    host.l2c_decoder_run.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_char_p)]
+    host.l2c_decoder_run.restype = ctypes.c_int
     _host = host
     return host
 
@@ -188,6 +198,26 @@ def to_bf16(out, inp, n, stream=None):
            "l2c_to_bf16")
 
 
+def decoder_init_model(embedding, classifier, norm_weight, width, vocab, stream=None):
+    _check(load().l2c_decoder_init_model(_vp(_ptr(embedding)), _vp(_ptr(classifier)),
+                                         _vp(_ptr(norm_weight)), width, vocab, _vp(_stream(stream))),
+           "l2c_decoder_init_model")
+
+
+def decoder_rmsnorm(normalized, tokens, embedding, weight, width, vocab, batch, stream=None):
+    _check(load().l2c_decoder_rmsnorm(_vp(_ptr(normalized)), _vp(_ptr(tokens)), _vp(_ptr(embedding)),
+                                      _vp(_ptr(weight)), width, vocab, batch, _vp(_stream(stream))),
+           "l2c_decoder_rmsnorm")
+
+
+def decoder_softmax_argmax(probabilities, logits, tokens, generated, vocab, batch, steps, step,
+                           stream=None):
+    _check(load().l2c_decoder_softmax_argmax(_vp(_ptr(probabilities)), _vp(_ptr(logits)),
+                                             _vp(_ptr(tokens)), _vp(_ptr(generated)), vocab, batch,
+                                             steps, step, _vp(_stream(stream))),
+           "l2c_decoder_softmax_argmax")
+
+
 def launch_shape(op, batch, cols, rows, variant=0):
     g, b, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     _check(load().l2c_launch_shape(op, batch, cols, rows, variant, ctypes.byref(g),
@@ -248,6 +278,34 @@ def compare_dumps(paths, in_process: bool = False):
         return host.l2c_compare_dumps(len(paths), arr), ""
     proc = subprocess.run([COMPARE] + list(paths), capture_output=True, text=True)
     return proc.returncode, proc.stdout + proc.stderr
+
+
+def decoder(args, in_process: bool = False, timeout=None):
+    """Runs the llama2c decoder application (the loom_private protocol);
+    returns (exit_code, record dict or None, stderr text).
+
+    args is the argument list after the program name, e.g.
+    ["--launch", "both", "--set", "batch=40", "--set", "width=96"].
+    In-process runs return no stderr text (it goes to the process's stderr).
+    """
+    import json
+    args = [str(a) for a in args]
+    if in_process:
+        host = load_host()
+        argv = [b"llama2c_decoder_hip"] + [a.encode() for a in args]
+        arr = (ctypes.c_char_p * len(argv))(*argv)
+        buf = ctypes.create_string_buffer(1 << 16)
+        code = host.l2c_decoder_main(len(argv), arr, buf, len(buf))
+        text = buf.value.decode()
+        return code, (json.loads(text) if text else None), ""
+    if not os.path.exists(DECODER):
+        raise FileNotFoundError(f"{DECODER} is not built")
+    proc = subprocess.run([DECODER] + args, capture_output=True, text=True, timeout=timeout)
+    record = None
+    for line in proc.stdout.splitlines():
+        if line.startswith("RESULT "):
+            record = json.loads(line[len("RESULT "):])
+    return proc.returncode, record, proc.stderr
 
 
 def command_line(args) -> str:

@@ -26,6 +26,10 @@
  *   l2c_matmul_q  no kernel in the reference: the quantized-weight matmul of the
  *                 benchmark configuration (MXFP4 / per-row fp8 weights, bf16
  *                 activations); its codes follow experiments/blackwell/lowprec/reference.cpp:13-96
+ *   l2c_decoder_init_model      init_model_kernel      applications/loom_private/decoder/decoder.cu:27-43
+ *   l2c_decoder_rmsnorm         rmsnorm_kernel         applications/loom_private/decoder/decoder.cu:45-77
+ *   l2c_decoder_softmax_argmax  softmax_argmax_kernel  applications/loom_private/decoder/decoder.cu:127-198
+ *   (the decoder's classifier_kernel, decoder.cu:79-125, is l2c_matmul)
  */
 #ifndef L2C_H
 #define L2C_H
@@ -123,6 +127,31 @@ int l2c_quantize_mxfp4(uint8_t *codes, uint8_t *scales, const float *W, int rows
 int l2c_quantize_fp8(uint8_t *codes, float *scales, const float *W, int rows, int cols,
                      hipStream_t stream);
 int l2c_to_bf16(uint16_t *out, const float *in, size_t n, hipStream_t stream);
+
+/*
+ * Batched greedy decoder (applications/loom_private/decoder): one step is
+ *   l2c_decoder_rmsnorm -> l2c_matmul(logits, normalized, classifier) ->
+ *   l2c_decoder_softmax_argmax
+ * over `batch` independent sequences whose current tokens live on the device.
+ *
+ * l2c_decoder_init_model: the synthetic model of the decoder's contract, on the
+ *   device: embedding[t][j] = (j == t ? 4 : 1), classifier[r][j] =
+ *   (j == (r + vocab - 1) % vocab ? 1 : 0) (both vocab x width), norm_weight = 1.
+ * l2c_decoder_rmsnorm: normalized[b][j] = weight[j] * (scale_b * E[t_b][j]) with
+ *   t_b = tokens[b], scale_b = 1 / sqrtf(sum_j E[t_b][j]^2 / width + 1e-5f); a token
+ *   outside [0, vocab) gives a NaN row.
+ * l2c_decoder_softmax_argmax: probabilities[b][r] = expf(logits[b][r] - max_b) / sum_b;
+ *   t = index of the first maximum probability (-1 if none); tokens[b] = t and
+ *   generated[b * steps + step] = t.
+ * Reductions run in a fixed order: results are deterministic.
+ */
+int l2c_decoder_init_model(float *embedding, float *classifier, float *norm_weight, int width,
+                           int vocab, hipStream_t stream);
+int l2c_decoder_rmsnorm(float *normalized, const int *tokens, const float *embedding,
+                        const float *weight, int width, int vocab, int batch, hipStream_t stream);
+int l2c_decoder_softmax_argmax(float *probabilities, const float *logits, int *tokens,
+                               int *generated, int vocab, int batch, int steps, int step,
+                               hipStream_t stream);
 
 /* Operations named by l2c_launch_shape. */
 enum l2c_op {

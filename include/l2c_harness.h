@@ -32,6 +32,23 @@ int l2c_harness_main(int argc, const char *const *argv, char *line, size_t capac
  */
 int l2c_compare_dumps(int count, const char *const *paths);
 
+/*
+ * The llama2c decoder application (loom-private/llama2c-decoder) under the
+ * loom_private protocol: argv as the llama2c_decoder_hip command line
+ * (--preset, --launch direct|graph|both, --action check|bench|profile,
+ * --iterations, --warmup, --set key=value, --asset, --json-out). Returns the
+ * exit code the executable would return: 0 pass, 1 output mismatch, 2 usage
+ * or invalid dimensions, 3 missing asset, 70 HIP error.
+ *   l2c_decoder_main writes the one-line JSON result record into
+ *     record[0..capacity) (empty if the run ended before it was built);
+ *   l2c_decoder_run prints "RESULT <record>" to stdout instead.
+ * Diagnostics go to stderr. Replaces main() of
+ * applications/loom_private/decoder/decoder.cu:411-412 with
+ * applications/loom_private/common/lp_harness.cuh:453-596.
+ */
+int l2c_decoder_main(int argc, const char *const *argv, char *record, size_t capacity);
+int l2c_decoder_run(int argc, const char *const *argv);
+
 #ifdef __cplusplus
 }
 #endif
