@@ -7,7 +7,8 @@ headline workload is the largest profiled shape, batch 1024 x dim 16384 x rows
 hipGraph, no copies: `value` is its microseconds per iteration (lower is
 better). The other benchmark configurations (decode GEMV 1 x 4096 x 11008,
 launch-bound 8 x 768 x 2048, the reference-compatible GEMV iteration at the
-large shape, the fused single launch, and the MXFP4 / fp8 weights) and the
+large shape, the fused single launch, the MXFP4 / fp8 weights, and the
+loom-private llama2c decoder application at its large shape) and the
 graph/direct and copy/nocopy splits are reported under "lines".
 
 The harness runs in this process (libl2c_host.so via ctypes): HIP events on
@@ -68,6 +69,29 @@ def summarize(name, rec):
         out["graph_capture_ms"] = rec["graph_capture_ms"]
         out["graph_instantiate_ms"] = rec["graph_instantiate_ms"]
     return out
+
+
+def decoder_line(l2c, mode, iterations=10, warmup=3):
+    """The llama2c decoder application at its contract's large shape (1024
+    sequences, width 16384, vocab 8192, 4 steps) under the loom_private bench
+    protocol; compute scope = token reset + 4 x (rmsnorm, classifier, softmax
+    + argmax)."""
+    t = time.time()
+    code, rec, _ = l2c.decoder(["--action", "bench", "--launch", mode, "--iterations", iterations,
+                                "--warmup", warmup], in_process=True)
+    if code != 0 or rec is None:
+        raise SystemExit(f"decoder bench failed (exit {code})")
+    comp, app = rec["timing"]["compute"], rec["timing"]["application"]
+    dims = rec["dimensions"]
+    flops = 2.0 * dims["classifier_macs_per_step"] * dims["steps"]
+    us = comp["batch_per_iteration_us"]
+    log(f"[bench] decoder {mode}: compute {us:.1f} us/invocation in {time.time() - t:.1f}s")
+    return {"name": f"decoder_large_{mode}", "mode": mode, "batch": dims["batch"], "width": dims["width"],
+            "vocab": dims["vocab"], "steps": dims["steps"], "iterations": iterations, "warmup": warmup,
+            "compute_us_per_invocation": us, "compute_single_median_us": comp["single_median_us"],
+            "application_us_per_invocation": app["batch_per_iteration_us"],
+            "classifier_tflops_compute_scope": flops / (us * 1e-6) / 1e12,
+            "note": "check-mode parity is a separate run (tests/test_decoder_gpu.py)"}
 
 
 def cpu_baseline(batch, size, rows, sample_vectors, sample_rows_norm):
@@ -154,6 +178,8 @@ def main():
         ]
         for name, a in plan:
             lines.append(summarize(name, run_line(l2c, a)))
+        for mode in ("graph", "direct"):
+            lines.append(decoder_line(l2c, mode))
 
     gemm_us = headline["matmul_us"]
     flops = 2.0 * B * R * S
