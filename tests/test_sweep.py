@@ -1,0 +1,79 @@
+"""The sweep tooling (l2c.sweep): config grammar, CSV columns and the derived
+speedup metrics of the reference's plot_sweep.py:29-73, on a synthetic CSV
+whose ratios are known (CPU); a two-config sweep on the GPU."""
+import csv
+import math
+
+import pytest
+
+from l2c import sweep
+
+
+def test_parse_config():
+    assert sweep.parse_config("1,16,16") == (1, 16, 16, 1, "copy")
+    assert sweep.parse_config("1024,256,8192,8,nocopy") == (1024, 256, 8192, 8, "nocopy")
+    with pytest.raises(ValueError):
+        sweep.parse_config("1,2")
+    with pytest.raises(ValueError):
+        sweep.parse_config("1,2,3,1,sometimes")
+
+
+def test_reference_config_sets():
+    # profile_cuda.sh:107-124: 9 launch-overhead configs, 10 GPU-filling configs.
+    assert len(sweep.SWEEP_CONFIGS.split()) == 9 and len(sweep.FILL_CONFIGS.split()) == 10
+    for c in sweep.SWEEP_CONFIGS.split() + sweep.FILL_CONFIGS.split():
+        sweep.parse_config(c)
+
+
+def _row(trial, mode, gpu, wall, submit, setup=(0.0, 0.0, 0.0), valid=1, code=0, batch=1):
+    r = dict.fromkeys(sweep.HEADER, "")
+    r.update(trial=trial, mode=mode, launches=30, batch=batch, size=16, rows=16, repeats=1,
+             copies="nocopy", matmul="naive", warmup_ms=100, gpu_ms_per_iter=gpu,
+             wall_ms_per_iter=wall, submit_us_per_iter=submit, graph_capture_ms=setup[0],
+             graph_instantiate_ms=setup[1], graph_upload_ms=setup[2], min_waves=0.5,
+             achieved_gbps=10, valid=valid, exit_code=code)
+    return r
+
+
+def test_speedup_metrics(tmp_path):
+    path = tmp_path / "sweep-x.csv"
+    rows = [
+        _row(1, "direct", 4.0, 4.5, 3.0), _row(1, "graph", 2.0, 2.5, 1.5, (0.5, 0.25, 0.25)),
+        _row(2, "graph", 2.0, 2.5, 1.0, (0.5, 0.25, 0.25)), _row(2, "direct", 3.0, 3.5, 3.0),
+        # an invalid run and a failed run are ignored
+        _row(3, "direct", 1.0, 1.0, 1.0, valid=0), _row(3, "graph", 9.0, 9.0, 9.0, code=1),
+        # a config with only one mode has no pair
+        _row(1, "direct", 1.0, 1.0, 1.0, batch=2),
+    ]
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=sweep.HEADER)
+        w.writeheader()
+        w.writerows(rows)
+    out = sweep.speedup_rows(str(path))
+    assert len(out) == 1
+    r = out[0]
+    assert r["trials"] == 2
+    assert math.isclose(r["gpu_speedup"], (2.0 + 1.5) / 2)
+    assert r["gpu_speedup_min"] == 1.5 and r["gpu_speedup_max"] == 2.0
+    assert math.isclose(r["submit_speedup"], (2.0 + 3.0) / 2)
+    assert math.isclose(r["graph_setup_ms"], 1.0)
+    # wall saving per replay = mean(4.5, 3.5) - mean(2.5, 2.5) = 1.5 ms -> ceil(1.0 / 1.5) = 1
+    assert r["break_even_replays"] == 1
+    out_path, _ = sweep.write_speedup(str(path))
+    assert out_path.endswith("sweep-x-speedup.csv")
+    with open(out_path) as f:
+        assert f.readline().startswith("batch,size,rows,repeats,copies,matmul,trials,")
+
+
+@pytest.mark.gpu
+def test_small_sweep_on_gpu(torch_gpu, tmp_path):
+    print("case sweep 2 configs x 1 trial", flush=True)
+    path = sweep.run_sweep("sweep", "1,64,64,1,nocopy 8,768,2048,2,copy", "20", "coalesced", trials=1,
+                           warmup_ms=20, out_dir=str(tmp_path), timeout=120)
+    with open(path) as f:
+        rows = list(csv.DictReader(f))
+    assert len(rows) == 4
+    assert all(r["exit_code"] == "0" and r["valid"] == "1" for r in rows)
+    assert [r["mode"] for r in rows] == ["direct", "graph", "direct", "graph"]
+    _, summary = sweep.write_speedup(path)
+    assert len(summary) == 2 and all(s["gpu_speedup"] > 0 for s in summary)
