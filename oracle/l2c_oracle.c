@@ -503,3 +503,119 @@ void orc_quantize_fp8(const float *W, int rows, int cols, uint8_t *codes, float 
   for (r = 0; r < rows; ++r)
     scales[r] = orc_quantize_fp8_row(W + (size_t)r * cols, cols, codes + (size_t)r * cols);
 }
+
+/* ------------------------------------------------------------------------ */
+/* MXFP6 and NVFP4 (experiments/blackwell/lowprec/spec.json "formats",       */
+/* "mxfp6", "nvfp4", "layout"), restated by brute force over all codes.      */
+
+/* OCP E3M2: sign bit 5, 3 exponent bits (bias 3), 2 mantissa bits, no
+ * infinity or NaN; exponent field 0 is subnormal m/4 * 2^-2; max 28. */
+static double e3m2_mag(unsigned c) {
+  const unsigned e = (c >> 2) & 7u, m = c & 3u;
+  return e == 0 ? ldexp(m / 4.0, -2) : ldexp(1.0 + m / 4.0, (int)e - 3);
+}
+
+double orc_e3m2_value(unsigned code) { return (code & 32u) ? -e3m2_mag(code) : e3m2_mag(code); }
+
+/* Nearest of the 32 magnitudes; a tie goes to the code whose least
+ * significant bit is 0; above 28 saturates; a zero magnitude is +0. */
+unsigned orc_e3m2_encode(double v) {
+  const double a = fabs(v);
+  unsigned best = 0, c;
+  if (a >= 28.0) return v < 0 ? 63u : 31u;
+  for (c = 1; c < 32; ++c) {
+    const double dc = fabs(a - e3m2_mag(c)), db = fabs(a - e3m2_mag(best));
+    if (dc < db || (dc == db && (best & 1u) && !(c & 1u))) best = c;
+  }
+  return (best != 0 && v < 0) ? (best | 32u) : best;
+}
+
+/* Shared exponent of an MXFP6 block with largest magnitude amax > 0:
+ * floor(log2(amax)) - 4, clamped to [-127, 127]; found by stepping, exact. */
+int orc_mxfp6_exponent(float amax) {
+  int e = -160;
+  while (ldexp(1.0, e + 1) <= (double)amax) ++e;
+  e -= 4;
+  return e < -127 ? -127 : e > 127 ? 127 : e;
+}
+
+/* One row (width % 32 == 0): element codes (unpacked, one per value) and one
+ * UE8M0 scale code per 32 values; a zero block has scale 0 and zero codes. */
+void orc_quantize_mxfp6_row(const float *x, int width, uint8_t *codes, uint8_t *scales) {
+  int blk, i;
+  for (blk = 0; blk * 32 < width; ++blk) {
+    float amax = 0.0f;
+    int e;
+    for (i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[blk * 32 + i]));
+    if (amax == 0.0f) {
+      scales[blk] = 0;
+      for (i = 0; i < 32; ++i) codes[blk * 32 + i] = 0;
+      continue;
+    }
+    e = orc_mxfp6_exponent(amax);
+    scales[blk] = (uint8_t)(e + 127);
+    for (i = 0; i < 32; ++i) codes[blk * 32 + i] = (uint8_t)orc_e3m2_encode(ldexp((double)x[blk * 32 + i], -e));
+  }
+}
+
+/* NVFP4 tensor scales: s = 2688 / a_t in float (1 for a_t = 0), d = 1 / s. */
+float orc_nvfp4_encode_scale(float tensor_amax) { return tensor_amax > 0.0f ? 2688.0f / tensor_amax : 1.0f; }
+float orc_nvfp4_decode_scale(float s) { return 1.0f / s; }
+
+/* One row (width % 16 == 0): block scale code = UE4M3((amax / 6) * s) and
+ * element codes E2M1((v * s) / f), every step a float operation in this
+ * order; a zero scale code zeroes the block's codes. */
+void orc_quantize_nvfp4_row(const float *x, int width, float s, uint8_t *codes, uint8_t *scales) {
+  int blk, i;
+  for (blk = 0; blk * 16 < width; ++blk) {
+    float amax = 0.0f, target, f;
+    unsigned sc;
+    for (i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[blk * 16 + i]));
+    target = amax / 6.0f;
+    target = target * s;
+    sc = orc_ue4m3_encode(target); /* non-negative: no sign bit */
+    scales[blk] = (uint8_t)sc;
+    f = (float)orc_ue4m3_value(sc);
+    for (i = 0; i < 16; ++i) {
+      float r;
+      if (sc == 0) {
+        codes[blk * 16 + i] = 0;
+        continue;
+      }
+      r = x[blk * 16 + i] * s;
+      r = r / f;
+      codes[blk * 16 + i] = (uint8_t)orc_e2m1_encode(r);
+    }
+  }
+}
+
+/* Packed E3M2 row: value i at bits 6i..6i+5 of a little-endian bit stream. */
+void orc_pack_e3m2(const uint8_t *codes, long long n, uint8_t *out) {
+  long long i;
+  memset(out, 0, (size_t)((n * 6 + 7) / 8));
+  for (i = 0; i < n; ++i) {
+    const long long bit = 6 * i;
+    const unsigned v = (unsigned)(codes[i] & 63u) << (bit % 8);
+    out[bit / 8] |= (uint8_t)(v & 0xffu);
+    if (bit % 8 > 2) out[bit / 8 + 1] |= (uint8_t)(v >> 8);
+  }
+}
+
+void orc_e3m2_encode_array(const double *v, size_t n, uint8_t *out) {
+  size_t i;
+  for (i = 0; i < n; ++i) out[i] = (uint8_t)orc_e3m2_encode(v[i]);
+}
+
+void orc_quantize_mxfp6(const float *X, int rows, int width, uint8_t *codes, uint8_t *scales) {
+  int r;
+  for (r = 0; r < rows; ++r)
+    orc_quantize_mxfp6_row(X + (size_t)r * width, width, codes + (size_t)r * width,
+                           scales + (size_t)r * (width / 32));
+}
+
+void orc_quantize_nvfp4(const float *X, int rows, int width, float s, uint8_t *codes, uint8_t *scales) {
+  int r;
+  for (r = 0; r < rows; ++r)
+    orc_quantize_nvfp4_row(X + (size_t)r * width, width, s, codes + (size_t)r * width,
+                           scales + (size_t)r * (width / 16));
+}

@@ -65,6 +65,14 @@ def lib():
     L.orc_quantize_mxfp4.argtypes = [_f32p, i, i, _u8p, _u8p]
     L.orc_quantize_fp8.argtypes = [_f32p, i, i, _u8p, _f32p]
     L.orc_qmatmul_ref.argtypes = [i, _u16p, _u8p, _c.c_void_p, i, i, _i32p, i, _f64p, _f64p]
+    L.orc_e3m2_value.argtypes, L.orc_e3m2_value.restype = [_c.c_uint], d
+    L.orc_e3m2_encode_array.argtypes = [_f64p, sz, _u8p]
+    L.orc_mxfp6_exponent.argtypes, L.orc_mxfp6_exponent.restype = [f], i
+    L.orc_quantize_mxfp6.argtypes = [_f32p, i, i, _u8p, _u8p]
+    L.orc_quantize_nvfp4.argtypes = [_f32p, i, i, f, _u8p, _u8p]
+    L.orc_nvfp4_encode_scale.argtypes, L.orc_nvfp4_encode_scale.restype = [f], f
+    L.orc_nvfp4_decode_scale.argtypes, L.orc_nvfp4_decode_scale.restype = [f], f
+    L.orc_pack_e3m2.argtypes = [_u8p, _c.c_longlong, _u8p]
     _orc = L
     return L
 
@@ -90,6 +98,12 @@ def ref():
     R.ref_encode_array.argtypes = [i, _f64p, sz, _u8p]
     R.ref_to_bf16_array.argtypes = [_f32p, sz, _u16p]
     R.ref_normals_stream1.argtypes = [i, _c.c_longlong, _f32p]
+    R.ref_quantize_mxfp6.argtypes = [_f32p, i, i, _u8p, _u8p]
+    R.ref_quantize_nvfp4.argtypes = [_f32p, i, i, f, _u8p, _u8p]
+    R.ref_nvfp4_encode_scale.argtypes, R.ref_nvfp4_encode_scale.restype = [f], f
+    R.ref_nvfp4_decode_scale.argtypes, R.ref_nvfp4_decode_scale.restype = [f], f
+    R.ref_unpack_e3m2.argtypes, R.ref_unpack_e3m2.restype = [_u8p, _c.c_longlong], _c.c_uint
+    R.ref_unpack_e2m1.argtypes, R.ref_unpack_e2m1.restype = [_u8p, _c.c_longlong], _c.c_uint
     _ref = R
     return R
 
@@ -219,6 +233,48 @@ def quantize_fp8(W, rows, cols):
     scales = np.empty(rows, np.float32)
     lib().orc_quantize_fp8(np.ascontiguousarray(W, np.float32), rows, cols, codes, scales)
     return codes, scales
+
+
+def e3m2_encode(v):
+    v = np.ascontiguousarray(v, np.float64)
+    out = np.empty(v.size, np.uint8)
+    lib().orc_e3m2_encode_array(v, v.size, out)
+    return out
+
+
+def e3m2_value(code):
+    return lib().orc_e3m2_value(int(code))
+
+
+def quantize_mxfp6(X, rows, width):
+    """Unpacked E3M2 codes [rows*width] and UE8M0 scale codes [rows*width/32]."""
+    codes = np.empty(rows * width, np.uint8)
+    scales = np.empty(rows * width // 32, np.uint8)
+    lib().orc_quantize_mxfp6(np.ascontiguousarray(X, np.float32), rows, width, codes, scales)
+    return codes, scales
+
+
+def nvfp4_scales(X):
+    """(encode s, decode d) of a tensor from its largest magnitude."""
+    a = np.float32(np.max(np.abs(np.asarray(X, np.float32)))) if np.size(X) else np.float32(0)
+    s = lib().orc_nvfp4_encode_scale(float(a))
+    return np.float32(s), np.float32(lib().orc_nvfp4_decode_scale(s))
+
+
+def quantize_nvfp4(X, rows, width, s):
+    """Unpacked E2M1 codes [rows*width] and UE4M3 scale codes [rows*width/16]."""
+    codes = np.empty(rows * width, np.uint8)
+    scales = np.empty(rows * width // 16, np.uint8)
+    lib().orc_quantize_nvfp4(np.ascontiguousarray(X, np.float32), rows, width, float(s), codes, scales)
+    return codes, scales
+
+
+def pack_e3m2(codes):
+    """Value i at bits 6i..6i+5 of a little-endian bit stream."""
+    c = np.ascontiguousarray(codes, np.uint8)
+    out = np.empty((c.size * 6 + 7) // 8, np.uint8)
+    lib().orc_pack_e3m2(c, c.size, out)
+    return out
 
 
 def pack_e2m1(codes):

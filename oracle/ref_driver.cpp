@@ -100,4 +100,21 @@ void ref_to_bf16_array(const float *v, size_t n, uint16_t *out) {
   for (size_t i = 0; i < n; ++i) out[i] = lowprec_ref::to_bf16(v[i]);
 }
 
+// The reference's MXFP6 / NVFP4 quantizers (experiments/blackwell/lowprec/reference.cpp).
+void ref_quantize_mxfp6(const float *X, int rows, int width, uint8_t *codes, uint8_t *scales) {
+  for (int r = 0; r < rows; ++r)
+    lowprec_ref::quantize_mxfp6(X + static_cast<size_t>(r) * width, width, codes + static_cast<size_t>(r) * width,
+                                scales + static_cast<size_t>(r) * (width / 32));
+}
+void ref_quantize_nvfp4(const float *X, int rows, int width, float s, uint8_t *codes, uint8_t *scales) {
+  for (int r = 0; r < rows; ++r)
+    lowprec_ref::quantize_nvfp4(X + static_cast<size_t>(r) * width, width, s, codes + static_cast<size_t>(r) * width,
+                                scales + static_cast<size_t>(r) * (width / 16));
+}
+float ref_nvfp4_encode_scale(float amax) { return lowprec_ref::nvfp4_encode_scale(amax); }
+float ref_nvfp4_decode_scale(float s) { return lowprec_ref::nvfp4_decode_scale(s); }
+// Values i of packed rows.
+unsigned ref_unpack_e3m2(const uint8_t *row, long long i) { return lowprec_ref::unpack_e3m2(row, i); }
+unsigned ref_unpack_e2m1(const uint8_t *row, long long i) { return lowprec_ref::unpack_e2m1(row, i); }
+
 }  // extern "C"

@@ -81,6 +81,31 @@ def main():
         R.ref_normals_stream1(seed, 64, out)
         g["normals"].append({"seed": seed, "stream": 1, "bits": out.view(np.uint32).tolist()})
 
+    # E3M2 encodings and the MXFP6 / NVFP4 quantizers (lowprec/reference.cpp:
+    # 27-45, 105-150) on the crafted edge-case matrix of lowprec_oracle.
+    import lowprec_oracle
+    ev = np.concatenate([np.arange(-33 * 16, 33 * 16 + 1) / 16.0, np.arange(-64, 65) / 256.0,
+                         [1e-9, -1e-9, 100.0, -100.0, 27.99, 28.0, 30.0, 30.01]]).astype(np.float64)
+    e3 = np.empty(ev.size, np.uint8)
+    R.ref_encode_array(1, ev, ev.size, e3)
+    g["e3m2"] = {"values": ev.tolist(), "codes": e3.tolist()}
+    rows, width = 40, 256
+    m = lowprec_oracle.crafted(rows, width)
+    c6 = np.empty(rows * width, np.uint8)
+    s6 = np.empty(rows * width // 32, np.uint8)
+    R.ref_quantize_mxfp6(m, rows, width, c6, s6)
+    amax = np.float32(np.abs(m).max())
+    enc = np.float32(R.ref_nvfp4_encode_scale(float(amax)))
+    dec = np.float32(R.ref_nvfp4_decode_scale(float(enc)))
+    c4 = np.empty(rows * width, np.uint8)
+    s4 = np.empty(rows * width // 16, np.uint8)
+    R.ref_quantize_nvfp4(m, rows, width, float(enc), c4, s4)
+    g["lowprec_crafted"] = {
+        "rows": rows, "width": width, "input_sha256": sha(m),
+        "mxfp6_codes_packed_hex": oracle.pack_e3m2(c6).tobytes().hex(), "mxfp6_scales_hex": s6.tobytes().hex(),
+        "nvfp4_encode_bits": int(enc.view(np.uint32)), "nvfp4_decode_bits": int(dec.view(np.uint32)),
+        "nvfp4_codes_packed_hex": oracle.pack_e2m1(c4).tobytes().hex(), "nvfp4_scales_hex": s4.tobytes().hex()}
+
     # A whole dump of the reference's writer (llama2c_common.h:321-345) for a
     # small random case, with outputs computed by the reference's validate_all
     # on the double-reference outputs rounded to float.

@@ -158,3 +158,62 @@ def test_normals_match(R, orc):
         ref = np.empty(1000, np.float32)
         R.ref_normals_stream1(seed, 1000, ref)
         np.testing.assert_array_equal(orc.normal(seed, 1, 0, 1000).view(np.uint32), ref.view(np.uint32))
+
+
+# --- MXFP6 / NVFP4 (experiments/blackwell/lowprec/reference.cpp:105-168) ----
+
+def _lowprec_inputs():
+    import lowprec_oracle as lo
+    yield "crafted", lo.crafted(130, 256)
+    emb, cls = lo.fixture(2, 1024, 16)
+    yield "fixture-embedding", emb
+    yield "fixture-classifier", cls
+    rng = np.random.default_rng(3)
+    wide = (rng.standard_normal((9, 4096)) * np.exp2(rng.integers(-20, 20, (9, 1)))).astype(np.float32)
+    yield "scaled-rows", wide
+
+
+def test_mxfp6_quantizer_matches(R, orc):
+    for name, m in _lowprec_inputs():
+        rows, width = m.shape
+        c, s = orc.quantize_mxfp6(m, rows, width)
+        c2 = np.empty_like(c)
+        s2 = np.empty_like(s)
+        R.ref_quantize_mxfp6(np.ascontiguousarray(m), rows, width, c2, s2)
+        np.testing.assert_array_equal(c, c2, err_msg=name)
+        np.testing.assert_array_equal(s, s2, err_msg=name)
+
+
+def test_nvfp4_quantizer_matches(R, orc):
+    for name, m in _lowprec_inputs():
+        rows, width = m.shape
+        enc, dec = orc.nvfp4_scales(m)
+        amax = float(np.float32(np.abs(m).max()))
+        assert np.float32(R.ref_nvfp4_encode_scale(amax)) == enc
+        assert np.float32(R.ref_nvfp4_decode_scale(float(enc))) == dec
+        c, s = orc.quantize_nvfp4(m, rows, width, enc)
+        c2 = np.empty_like(c)
+        s2 = np.empty_like(s)
+        R.ref_quantize_nvfp4(np.ascontiguousarray(m), rows, width, float(enc), c2, s2)
+        np.testing.assert_array_equal(c, c2, err_msg=name)
+        np.testing.assert_array_equal(s, s2, err_msg=name)
+    assert R.ref_nvfp4_encode_scale(0.0) == 1.0
+
+
+def test_packing_matches_reference_unpack(R, orc):
+    rng = np.random.default_rng(9)
+    c6 = rng.integers(0, 64, 4 * 96).astype(np.uint8)
+    p6 = orc.pack_e3m2(c6)
+    assert p6.size == c6.size * 3 // 4
+    assert [R.ref_unpack_e3m2(p6, i) for i in range(c6.size)] == c6.tolist()
+    c4 = rng.integers(0, 16, 256).astype(np.uint8)
+    p4 = orc.pack_e2m1(c4)
+    assert [R.ref_unpack_e2m1(p4, i) for i in range(c4.size)] == c4.tolist()
+
+
+def test_e3m2_encoder_matches(R, orc):
+    v = np.concatenate([np.linspace(-40, 40, 20001), np.ldexp(np.arange(-64, 65) / 8.0, -4)])
+    ours = orc.e3m2_encode(v)
+    theirs = np.empty(v.size, np.uint8)
+    R.ref_encode_array(1, np.ascontiguousarray(v, np.float64), v.size, theirs)
+    np.testing.assert_array_equal(ours, theirs)
