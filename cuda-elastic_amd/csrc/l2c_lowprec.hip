@@ -1,0 +1,236 @@
+// Device quantizers of the low-precision classifier cases: MXFP6 (E3M2 with
+// UE8M0 scales per 32 values), NVFP4 (E2M1 with UE4M3 scales per 16 values
+// and FP32 tensor scales) and BF16
+// (experiments/blackwell/lowprec/spec.json "mxfp6", "nvfp4", "layout";
+// the reference's kernels are decoder_lowprec.cu:202-340).
+//
+// Layouts (row-major [rows][width], width along K):
+//  * MXFP6 codes: a little-endian bit stream per row, value i at bits
+//    6i..6i+5, so 32 values are 24 bytes and a row is width * 3 / 4 bytes.
+//    Scales: one byte per block, [rows][width / 32] (the reference stores
+//    them in CUTLASS's tile layout for its GEMM; the byte values are the
+//    same, and this layout is the one the MXFP6 GEMM here reads).
+//  * NVFP4 codes: two per byte, even index in the low nibble, [rows][width / 2].
+//    Scales: [rows][width / 16] UE4M3 bytes. Tensor scales: s = 2688 / a_t
+//    (1 when a_t = 0) and d = 1 / s, both FP32.
+//  * NVFP4 bf16 expansion (optional): [rows][width] bf16 of each element's
+//    value times its block scale (d apart). The product of an E2M1 magnitude
+//    (at most 2 significant bits) and a UE4M3 value (at most 4) has at most 6
+//    significant bits and lies in [2^-10, 2688], so the bf16 value is exact:
+//    it is the operand form the bf16 matrix cores multiply.
+//
+// Every quantizer reads its input once, coalesced: a group of 8 (MXFP6) or 4
+// (NVFP4) lanes shares one block, each lane holding 4 consecutive floats;
+// the block maximum is a butterfly over the group.
+#include "l2c_common.h"
+#include "l2c_formats.h"
+#include "../../include/l2c.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kAmaxBlocks = 1024;  // partial maxima of the tensor-scale pass
+
+__device__ __forceinline__ float group_max(float v, int lanes) {
+  for (int off = 1; off < lanes; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, L2C_WAVE));
+  return v;
+}
+
+// One group of 8 lanes per 32-value block; blocks are numbered row-major, so
+// block b covers x[32 b ..], codes[24 b ..] and scales[b].
+__global__ __launch_bounds__(kThreads) void quantize_mxfp6_kernel(uint8_t *__restrict__ codes,
+                                                                  uint8_t *__restrict__ scales,
+                                                                  const float *__restrict__ x,
+                                                                  long long blocks) {
+  const long long gid = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+  const long long blk = gid / 8;
+  const int j = static_cast<int>(gid % 8);
+  const bool live = blk < blocks;
+  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (live) v = reinterpret_cast<const float4 *>(x)[blk * 8 + j];
+  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  amax = group_max(amax, 8);
+  const int X = l2c::mxfp6_exponent(amax);
+  const float inv = l2c::pow2_neg(X);
+  unsigned p = 0;
+  if (amax > 0.0f) {
+    p = l2c::e3m2_code(v.x * inv) | (l2c::e3m2_code(v.y * inv) << 6) | (l2c::e3m2_code(v.z * inv) << 12) |
+        (l2c::e3m2_code(v.w * inv) << 18);
+  }
+  // Lane j holds bits 24j..24j+23 of the block's 192; lane d < 6 writes dword
+  // d = bits 32d..32d+31, taken from lanes lo = 4d / 3 and lo + 1.
+  const int base = (threadIdx.x % L2C_WAVE) & ~7;
+  const int d = j < 6 ? j : 5;
+  const int lo = (4 * d) / 3, off = 32 * d - 24 * lo;
+  const unsigned plo = static_cast<unsigned>(__shfl(static_cast<int>(p), base + lo, L2C_WAVE));
+  const unsigned phi = static_cast<unsigned>(__shfl(static_cast<int>(p), base + lo + 1, L2C_WAVE));
+  const unsigned word = (plo >> off) | (phi << (24 - off));
+  if (live && j < 6) reinterpret_cast<unsigned *>(codes + blk * 24)[j] = word;
+  if (live && j == 0) scales[blk] = amax > 0.0f ? static_cast<uint8_t>(X + 127) : 0;
+}
+
+// Partial maxima of |x| over a grid-stride walk; one per workgroup.
+__global__ __launch_bounds__(kThreads) void amax_partials_kernel(float *__restrict__ partials,
+                                                                 const float *__restrict__ x,
+                                                                 long long n) {
+  __shared__ float slots[kThreads / L2C_WAVE];
+  float m = 0.0f;
+  const long long n4 = n / 4;
+  const long long stride = static_cast<long long>(gridDim.x) * kThreads;
+  for (long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < n4; i += stride) {
+    const float4 v = reinterpret_cast<const float4 *>(x)[i];
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  for (long long i = 4 * n4 + static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride)
+    m = fmaxf(m, fabsf(x[i]));
+  m = l2c::block_max(m, slots);
+  if (threadIdx.x == 0) partials[blockIdx.x] = m;
+}
+
+// The tensor maximum from the partials, then s = 2688 / a_t (1 for a_t = 0),
+// d = 1 / s, and alpha = d * other_decode when asked (FP32, IEEE division).
+__global__ __launch_bounds__(kThreads) void nvfp4_scales_kernel(float *__restrict__ tensor_scales,
+                                                                float *__restrict__ alpha,
+                                                                const float *__restrict__ other_decode,
+                                                                const float *__restrict__ partials,
+                                                                int count) {
+#pragma clang fp contract(off)
+  __shared__ float slots[kThreads / L2C_WAVE];
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < count; i += kThreads) m = fmaxf(m, partials[i]);
+  m = l2c::block_max(m, slots);
+  if (threadIdx.x == 0) {
+    const float s = l2c::nvfp4_encode_scale(m);
+    const float d = 1.0f / s;
+    tensor_scales[0] = s;
+    tensor_scales[1] = d;
+    if (alpha) *alpha = d * *other_decode;
+  }
+}
+
+// One group of 4 lanes per 16-value block: scale code UE4M3((a / 6) s), codes
+// E2M1((v s) / f), each step an FP32 operation in this order; a zero scale
+// code zeroes the block. Optionally also the exact bf16 values code * f.
+__global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(uint8_t *__restrict__ codes,
+                                                                  uint8_t *__restrict__ scales,
+                                                                  uint16_t *__restrict__ expanded,
+                                                                  const float *__restrict__ x,
+                                                                  const float *__restrict__ tensor_scales,
+                                                                  long long blocks) {
+#pragma clang fp contract(off)
+  const long long gid = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+  const long long blk = gid / 4;
+  const int j = static_cast<int>(gid % 4);
+  const bool live = blk < blocks;
+  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (live) v = reinterpret_cast<const float4 *>(x)[blk * 4 + j];
+  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  amax = group_max(amax, 4);
+  const float s = tensor_scales[0];
+  const unsigned sc = l2c::nvfp4_scale_code(amax, s);
+  const float f = l2c::ue4m3_value(sc);
+  const float e[4] = {v.x, v.y, v.z, v.w};
+  unsigned c[4] = {0, 0, 0, 0};
+  if (sc != 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = l2c::nvfp4_code(e[i], s, f);
+  }
+  if (!live) return;
+  reinterpret_cast<uint16_t *>(codes)[blk * 4 + j] =
+      static_cast<uint16_t>(c[0] | (c[1] << 4) | (c[2] << 8) | (c[3] << 12));
+  if (j == 0) scales[blk] = static_cast<uint8_t>(sc);
+  if (expanded) {
+    unsigned b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = __float_as_uint(l2c::e2m1_value(c[i]) * f) >> 16;  // exact
+    reinterpret_cast<uint2 *>(expanded)[blk * 4 + j] = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+  }
+}
+
+// BF16 round to nearest even, four values a thread (finite values never
+// round to infinity: reference.cpp:84-96 picks between the truncation and the
+// next finite magnitude).
+__device__ __forceinline__ unsigned bf16_rne(float f) {
+  const unsigned bits = __float_as_uint(f);
+  if ((bits & 0x7f800000u) == 0x7f800000u) return bits >> 16;
+  unsigned r = (bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16;
+  if ((r & 0x7fffu) == 0x7f80u) --r;
+  return r;
+}
+
+__global__ __launch_bounds__(kThreads) void to_bf16_x4_kernel(uint2 *__restrict__ out,
+                                                              const float4 *__restrict__ in,
+                                                              long long n4) {
+  const long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n4) return;
+  const float4 v = in[i];
+  out[i] = make_uint2(bf16_rne(v.x) | (bf16_rne(v.y) << 16), bf16_rne(v.z) | (bf16_rne(v.w) << 16));
+}
+
+bool grid_ok(long long threads, unsigned *grid) {
+  const long long g = (threads + kThreads - 1) / kThreads;
+  if (g > 0x7fffffffLL) return false;
+  *grid = static_cast<unsigned>(g);
+  return true;
+}
+
+}  // namespace
+
+extern "C" int l2c_quantize_mxfp6(uint8_t *codes, uint8_t *scales, const float *x, int rows, int width,
+                                  hipStream_t stream) {
+  if (rows < 0 || width <= 0 || width % 32 != 0) return hipErrorInvalidValue;
+  if (rows == 0) return hipSuccess;
+  if (!codes || !scales || !x || !l2c_aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 3u))
+    return hipErrorInvalidValue;
+  const long long blocks = static_cast<long long>(rows) * (width / 32);
+  unsigned grid;
+  if (!grid_ok(blocks * 8, &grid)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(quantize_mxfp6_kernel, dim3(grid), dim3(kThreads), 0, stream, codes, scales, x, blocks);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+extern "C" int l2c_nvfp4_tensor_scales(float *tensor_scales, float *alpha, const float *other_decode,
+                                       const float *x, long long n, float *partials, hipStream_t stream) {
+  if (n < 0 || !tensor_scales || !partials || (n > 0 && !x) || (alpha && !other_decode))
+    return hipErrorInvalidValue;
+  if (x && !l2c_aligned16(x)) return hipErrorInvalidValue;
+  const long long want = (n / 4 + kThreads - 1) / kThreads;
+  const int parts = static_cast<int>(want < 1 ? 1 : want > kAmaxBlocks ? kAmaxBlocks : want);
+  hipLaunchKernelGGL(amax_partials_kernel, dim3(parts), dim3(kThreads), 0, stream, partials, x, n);
+  L2C_LAUNCH_CHECK();
+  hipLaunchKernelGGL(nvfp4_scales_kernel, dim3(1), dim3(kThreads), 0, stream, tensor_scales, alpha,
+                     other_decode, static_cast<const float *>(partials), parts);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+extern "C" int l2c_quantize_nvfp4(uint8_t *codes, uint8_t *scales, uint16_t *expanded_bf16, const float *x,
+                                  const float *tensor_scales, int rows, int width, hipStream_t stream) {
+  if (rows < 0 || width <= 0 || width % 16 != 0) return hipErrorInvalidValue;
+  if (rows == 0) return hipSuccess;
+  if (!codes || !scales || !x || !tensor_scales || !l2c_aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 1u) ||
+      (expanded_bf16 && (reinterpret_cast<uintptr_t>(expanded_bf16) & 7u)))
+    return hipErrorInvalidValue;
+  const long long blocks = static_cast<long long>(rows) * (width / 16);
+  unsigned grid;
+  if (!grid_ok(blocks * 4, &grid)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(quantize_nvfp4_kernel, dim3(grid), dim3(kThreads), 0, stream, codes, scales, expanded_bf16,
+                     x, tensor_scales, blocks);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+// The vectorized form of l2c_to_bf16 (l2c_qgemm.hip) for 16-byte aligned
+// inputs whose length is a multiple of 4.
+extern "C" int l2c_to_bf16_x4(uint16_t *out, const float *in, long long n, hipStream_t stream) {
+  if (n < 0 || n % 4 != 0) return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  if (!out || !in || !l2c_aligned16(in) || (reinterpret_cast<uintptr_t>(out) & 7u)) return hipErrorInvalidValue;
+  unsigned grid;
+  if (!grid_ok(n / 4, &grid)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(to_bf16_x4_kernel, dim3(grid), dim3(kThreads), 0, stream, reinterpret_cast<uint2 *>(out),
+                     reinterpret_cast<const float4 *>(in), n / 4);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}

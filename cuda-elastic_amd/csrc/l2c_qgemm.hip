@@ -1,6 +1,8 @@
 // Quantized-weight contraction out[b][r] = sum_k X[b][k] * deq(W)[r][k] with
-// bf16 activations and MXFP4 or per-row-scaled fp8 e4m3 weights, plus the
-// device quantizers that produce those weights.
+// bf16 activations and MXFP4, per-row-scaled fp8 e4m3 or bf16 weights, plus
+// the device quantizers that produce those weights. The bf16-weight form is
+// the classifier of the lowprec bf16 and NVFP4 cases (an optional device
+// alpha multiplies each output).
 //
 // Kernel design (gfx950):
 //  * The activations are bf16 and must stay bf16 (the oracle multiplies the
@@ -46,6 +48,7 @@
 #include <type_traits>
 
 #include "l2c_common.h"
+#include "l2c_formats.h"
 #include "../../include/l2c.h"
 
 namespace {
@@ -72,58 +75,29 @@ constexpr long long kMaxTileBytes = 0xffffffffLL;
 // Per-format staging geometry. W rows hold the step's codes (32 bytes of
 // MXFP4 or 64 of fp8) with 16-byte chunks XOR-swizzled by row bits; MXFP4
 // block scales follow as fp32 [kBN][2].
+constexpr int kFmtBf16 = 2;  // bf16 weights (l2c_matmul_bf16)
+
 template <int FMT>
 struct Geometry {
-  static constexpr int kWRow = FMT == L2C_Q_MXFP4 ? 32 : 64;  // code bytes per W row and step
+  // Code bytes per W row and step: 64 k of MXFP4, fp8 or bf16.
+  static constexpr int kWRow = FMT == L2C_Q_MXFP4 ? 32 : FMT == L2C_Q_FP8 ? 64 : 128;
   static constexpr int kWBytes = kWRow * kBN / kThreads;      // code bytes staged per thread
-  static constexpr int kWReads = FMT == L2C_Q_MXFP4 ? 1 : 2;  // 16-byte code reads per block
+  static constexpr int kWReads = kWRow / 32;                  // 16-byte code reads per block
   static constexpr int kXStage = kBM * kXStride;
   static constexpr int kSStage = kXStage + kBN * kWRow;
   static constexpr int kStage = kSStage + (FMT == L2C_Q_MXFP4 ? kBN * 8 : 0);
   // Chunk swizzle: 16 lanes reading chunk c of 16 consecutive rows (or 32
   // lanes storing 8 rows) touch 64 distinct banks.
   static __device__ __forceinline__ int swizzle(int row) {
-    return FMT == L2C_Q_MXFP4 ? (row >> 3) & 1 : (row >> 2) & 3;
+    return FMT == L2C_Q_MXFP4 ? (row >> 3) & 1 : FMT == L2C_Q_FP8 ? (row >> 2) & 3 : (row >> 1) & 7;
   }
 };
 
 // ---------------------------------------------------------------------------
 // Element encoders / decoders.
 
-__device__ __forceinline__ unsigned e2m1_code(float v) {
-  const float t = fabsf(v);
-  unsigned c;
-  if (t <= 0.25f) c = 0;
-  else if (t < 0.75f) c = 1;
-  else if (t <= 1.25f) c = 2;
-  else if (t < 1.75f) c = 3;
-  else if (t <= 2.5f) c = 4;
-  else if (t < 3.5f) c = 5;
-  else if (t <= 5.0f) c = 6;
-  else c = 7;
-  return (c != 0 && v < 0.0f) ? (c | 8u) : c;
-}
-
-__device__ __forceinline__ unsigned e4m3_code(float v) {
-  const float a = fabsf(v);
-  unsigned c;
-  if (a < 0.015625f) {  // below 2^-6: subnormal codes m * 2^-9, m in 0..8
-    c = static_cast<unsigned>(rintf(a * 512.0f));
-  } else {
-    const unsigned bits = __float_as_uint(a);
-    int e = static_cast<int>((bits >> 23) & 0xffu) - 127;
-    unsigned q = (bits >> 20) & 7u;
-    const unsigned rem = bits & 0xfffffu;
-    if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) ++q;
-    if (q == 8u) {
-      q = 0;
-      ++e;
-    }
-    c = e > 8 ? 0x7eu : ((static_cast<unsigned>(e + 7) << 3) | q);
-    if (c > 0x7eu) c = 0x7eu;
-  }
-  return (c != 0 && v < 0.0f) ? (c | 0x80u) : c;
-}
+using l2c::e2m1_code;
+using l2c::e4m3_code;
 
 __device__ __forceinline__ int mxfp4_exponent(float amax) {
   const unsigned bits = __float_as_uint(amax);
@@ -218,7 +192,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
   const int r = lane % 32;
   const int h = lane / 32;
 
-  const int wrow_bytes = FMT == L2C_Q_MXFP4 ? K / 2 : K;
+  const int wrow_bytes = FMT == L2C_Q_MXFP4 ? K / 2 : FMT == L2C_Q_FP8 ? K : 2 * K;
   const __amdgpu_buffer_rsrc_t rx =
       l2c::buffer_rsrc(X + static_cast<size_t>(m0) * K, static_cast<uint32_t>(mrows) * K * 2u);
   const __amdgpu_buffer_rsrc_t rw =
@@ -240,6 +214,8 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
   const int wbyte = G::kWBytes * (tid % (G::kWRow / G::kWBytes));
   const int wg = min(wrow, nrows - 1) * wrow_bytes + wbyte;
   const int ws = G::kXStage + wrow * G::kWRow + (((wbyte >> 4) ^ G::swizzle(wrow)) << 4) + (wbyte & 15);
+  // bf16: the thread's second 16-byte chunk.
+  const int ws1 = G::kXStage + wrow * G::kWRow + ((((wbyte >> 4) + 1) ^ G::swizzle(wrow)) << 4);
   // MXFP4 scales: threads t and t + 256 stage the same (row, half) word.
   const int srow = (tid & 255) / 2, shalf = tid & 1;
   const int sg = min(srow, nrows - 1) * (K / 32) + shalf;
@@ -247,14 +223,16 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
 
   u32x4 gx[2][kXChunks];
   u32x4 gw4[2];
+  u32x4 gw8[2];
   u32x2 gw2[2];
   uint32_t gs[2];
   auto gload = [&](auto set, int t) __attribute__((always_inline)) {
     constexpr int st = decltype(set)::value;
 #pragma unroll
     for (int v = 0; v < kXChunks; ++v) gx[st][v] = __builtin_amdgcn_raw_buffer_load_b128(rx, xg[v], 128 * t, 0);
-    if constexpr (G::kWBytes == 16) gw4[st] = __builtin_amdgcn_raw_buffer_load_b128(rw, wg, G::kWRow * t, 0);
+    if constexpr (G::kWBytes >= 16) gw4[st] = __builtin_amdgcn_raw_buffer_load_b128(rw, wg, G::kWRow * t, 0);
     else gw2[st] = __builtin_amdgcn_raw_buffer_load_b64(rw, wg, G::kWRow * t, 0);
+    if constexpr (G::kWBytes == 32) gw8[st] = __builtin_amdgcn_raw_buffer_load_b128(rw, wg + 16, G::kWRow * t, 0);
     if constexpr (FMT == L2C_Q_MXFP4) gs[st] = __builtin_amdgcn_raw_buffer_load_b8(rs, sg, 2 * t, 0);
   };
   auto lstore = [&](auto set, int stage) __attribute__((always_inline)) {
@@ -262,8 +240,9 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
     unsigned char *base = lds + stage * G::kStage;
 #pragma unroll
     for (int v = 0; v < kXChunks; ++v) *reinterpret_cast<u32x4 *>(base + xs[v]) = gx[st][v];
-    if constexpr (G::kWBytes == 16) *reinterpret_cast<u32x4 *>(base + ws) = gw4[st];
+    if constexpr (G::kWBytes >= 16) *reinterpret_cast<u32x4 *>(base + ws) = gw4[st];
     else *reinterpret_cast<u32x2 *>(base + ws) = gw2[st];
+    if constexpr (G::kWBytes == 32) *reinterpret_cast<u32x4 *>(base + ws1) = gw8[st];
     if constexpr (FMT == L2C_Q_MXFP4) {
       // Block scale 2^(s - 127) as fp32 (s = 0 is the subnormal 2^-127).
       const uint32_t e = gs[st] & 0xffu;
@@ -295,7 +274,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
 #pragma unroll
       for (int v = 0; v < G::kWReads; ++v) {
         const int row = brow + 32 * j;
-        const int chunk = (FMT == L2C_Q_MXFP4 ? h : 2 * h + v) ^ G::swizzle(row);
+        const int chunk = (G::kWReads * h + v) ^ G::swizzle(row);
         f.w[j][v] = *reinterpret_cast<const u32x4 *>(base + G::kXStage + row * G::kWRow + 16 * chunk);
       }
       if constexpr (FMT == L2C_Q_MXFP4)
@@ -323,6 +302,11 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
           d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 1));
           d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 2));
           d[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 3));
+        } else if constexpr (FMT == kFmtBf16) {
+          d[0] = kok ? f.w[j][q][0] : 0u;
+          d[1] = kok ? f.w[j][q][1] : 0u;
+          d[2] = kok ? f.w[j][q][2] : 0u;
+          d[3] = kok ? f.w[j][q][3] : 0u;
         } else {
           const uint32_t c0 = kok ? f.w[j][q / 2][2 * (q % 2)] : 0u;
           const uint32_t c1 = kok ? f.w[j][q / 2][2 * (q % 2) + 1] : 0u;
@@ -390,8 +374,9 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
     }
     const int half = G::kWRow / 2;
     const int wgo = wg - (wbyte >= half ? half : 0);
-    if constexpr (G::kWBytes == 16) gw4[0] = __builtin_amdgcn_raw_buffer_load_b128(rw, wgo, G::kWRow * t2, 0);
+    if constexpr (G::kWBytes >= 16) gw4[0] = __builtin_amdgcn_raw_buffer_load_b128(rw, wgo, G::kWRow * t2, 0);
     else gw2[0] = __builtin_amdgcn_raw_buffer_load_b64(rw, wgo, G::kWRow * t2, 0);
+    if constexpr (G::kWBytes == 32) gw8[0] = __builtin_amdgcn_raw_buffer_load_b128(rw, wgo + 16, G::kWRow * t2, 0);
     if constexpr (FMT == L2C_Q_MXFP4) gs[0] = __builtin_amdgcn_raw_buffer_load_b8(rs, sg - shalf, 2 * t2, 0);
     lstore(I0(), 0);
     __syncthreads();
@@ -404,6 +389,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
     const int n = brow + 32 * j;
     float rs_ = 1.0f;
     if constexpr (FMT == L2C_Q_FP8) rs_ = n < nrows ? static_cast<const float *>(scales)[n0 + n] : 0.0f;
+    if constexpr (FMT == kFmtBf16) rs_ = scales ? *static_cast<const float *>(scales) : 1.0f;  // alpha
 #pragma unroll
     for (int i = 0; i < kFragM; ++i) {
 #pragma unroll
@@ -483,6 +469,21 @@ extern "C" int l2c_to_bf16(uint16_t *out, const float *in, size_t n, hipStream_t
   if (grid > 0x7fffffffULL) return hipErrorInvalidValue;
   hipLaunchKernelGGL(to_bf16_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream, out,
                      in, n);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+extern "C" int l2c_matmul_bf16(float *out, const uint16_t *X, const uint16_t *W, const float *alpha, int batch,
+                               int cols, int rows, hipStream_t stream) {
+  if (batch < 0 || cols <= 0 || rows < 0 || cols % 32 != 0) return hipErrorInvalidValue;
+  if (batch == 0 || rows == 0) return hipSuccess;
+  if (!out || !X || !W || !l2c_aligned16(X) || !l2c_aligned16(W)) return hipErrorInvalidValue;
+  if (static_cast<long long>(kBM) * cols * 2 > kMaxTileBytes) return hipErrorInvalidValue;
+  const long long tiles =
+      static_cast<long long>((batch + kBM - 1) / kBM) * ((rows + kBN - 1) / kBN);
+  if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(qgemm_kernel<kFmtBf16>, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream, out,
+                     X, reinterpret_cast<const uint8_t *>(W), static_cast<const void *>(alpha), batch, rows, cols);
   L2C_LAUNCH_CHECK();
   return hipSuccess;
 }

@@ -7,6 +7,9 @@
 //
 //   l2c_kernel_bench OP BATCH SIZE ROWS ITERS   (after >= 100 ms of warm-up launches)
 //   OP: rmsnorm softmax gemv naive fused matmul mxfp4 fp8 copy
+//       bf16 mxfp6 (lowprec classifier contractions, alpha on for bf16)
+//       cvt_bf16 cvt_mxfp6 cvt_nvfp4 (lowprec per-step activation conversions
+//       of BATCH x SIZE; cvt_nvfp4 = tensor scales + codes + bf16 expansion)
 //
 // `copy` runs a plain 16-byte-per-lane copy of BATCH x SIZE floats (read
 // once, written once): the calibration kernel for the FETCH_SIZE/WRITE_SIZE
@@ -86,9 +89,33 @@ int main(int argc, char **argv) {
   if (m) hipLaunchKernelGGL(fill_kernel, dim3(4096), dim3(256), 0, nullptr, m, mat, 4u, 1.0f / 128.0f);
   CHECK(hipGetLastError());
 
-  uint16_t *xb = nullptr;
-  uint8_t *codes = nullptr, *sc8 = nullptr;
-  float *sc32 = nullptr;
+  uint16_t *xb = nullptr, *wb = nullptr;
+  uint8_t *codes = nullptr, *sc8 = nullptr, *xq = nullptr, *xs = nullptr;
+  float *sc32 = nullptr, *alpha = nullptr, *partials = nullptr, *tscales = nullptr;
+  if (op == "bf16" || op == "mxfp6" || op == "cvt_bf16" || op == "cvt_mxfp6" || op == "cvt_nvfp4") {
+    if (S % 128 != 0) {
+      std::fprintf(stderr, "lowprec ops need SIZE %% 128 == 0\n");
+      return 2;
+    }
+    CHECK(hipMalloc(&xb, vec * 2));
+    CHECK(hipMalloc(&xq, vec));
+    CHECK(hipMalloc(&xs, vec / 16));
+    CHECK(hipMalloc(&alpha, 4));
+    CHECK(hipMalloc(&tscales, 8));
+    CHECK(hipMalloc(&partials, L2C_NVFP4_PARTIALS * 4));
+    const float one = 0.5f;
+    CHECK(hipMemcpy(alpha, &one, 4, hipMemcpyHostToDevice));
+    if (op == "bf16") {
+      CHECK(hipMalloc(&wb, mat * 2));
+      L2C(l2c_to_bf16_x4(xb, x, static_cast<long long>(vec), nullptr));
+      L2C(l2c_to_bf16_x4(wb, m, static_cast<long long>(mat), nullptr));
+    } else if (op == "mxfp6") {
+      CHECK(hipMalloc(&codes, mat * 3 / 4));
+      CHECK(hipMalloc(&sc8, mat / 32));
+      L2C(l2c_quantize_mxfp6(xq, xs, x, B, S, nullptr));
+      L2C(l2c_quantize_mxfp6(codes, sc8, m, R, S, nullptr));
+    }
+  }
   if (op == "mxfp4" || op == "fp8") {
     if (S % 32 != 0) {
       std::fprintf(stderr, "quantized ops need SIZE %% 32 == 0\n");
@@ -135,6 +162,24 @@ int main(int argc, char **argv) {
       bytes = vec * 2.0 + (op == "mxfp4" ? mat / 2.0 + mat / 32.0 : mat + R * 4.0) +
               static_cast<double>(B) * R * 4;
       flops = 2.0 * B * static_cast<double>(mat);
+    } else if (op == "bf16") {
+      L2C(l2c_matmul_bf16(prod, xb, wb, alpha, B, S, R, s));
+      bytes = (vec + static_cast<double>(mat)) * 2 + static_cast<double>(B) * R * 4;
+      flops = 2.0 * B * static_cast<double>(mat);
+    } else if (op == "mxfp6") {
+      L2C(l2c_matmul_mxfp6(prod, xq, xs, codes, sc8, B, S, R, s));
+      bytes = (vec + static_cast<double>(mat)) * (0.75 + 1.0 / 32) + static_cast<double>(B) * R * 4;
+      flops = 2.0 * B * static_cast<double>(mat);
+    } else if (op == "cvt_bf16") {
+      L2C(l2c_to_bf16_x4(xb, x, static_cast<long long>(vec), s));
+      bytes = vec * 6.0;
+    } else if (op == "cvt_mxfp6") {
+      L2C(l2c_quantize_mxfp6(xq, xs, x, B, S, s));
+      bytes = vec * (4.0 + 0.75 + 1.0 / 32);
+    } else if (op == "cvt_nvfp4") {
+      L2C(l2c_nvfp4_tensor_scales(tscales, alpha, tscales + 1, x, static_cast<long long>(vec), partials, s));
+      L2C(l2c_quantize_nvfp4(xq, xs, xb, x, tscales, B, S, s));
+      bytes = vec * (4.0 + 4.0 + 0.5 + 1.0 / 16 + 2.0);
     } else if (op == "copy") {
       hipLaunchKernelGGL(copy_kernel, dim3(4096), dim3(256), 0, s, reinterpret_cast<float4 *>(o1),
                          reinterpret_cast<const float4 *>(x), vec / 4);

@@ -41,7 +41,10 @@ KERNEL_SYMBOLS = (
     "l2c_quantize_mxfp4", "l2c_quantize_fp8", "l2c_to_bf16", "l2c_launch_shape",
     "l2c_strerror", "l2c_version",
     "l2c_decoder_init_model", "l2c_decoder_rmsnorm", "l2c_decoder_softmax_argmax",
+    "l2c_quantize_mxfp6", "l2c_nvfp4_tensor_scales", "l2c_quantize_nvfp4", "l2c_to_bf16_x4",
+    "l2c_matmul_bf16", "l2c_matmul_mxfp6",
 )
+NVFP4_PARTIALS = 1024  # L2C_NVFP4_PARTIALS
 HOST_SYMBOLS = ("l2c_harness_main", "l2c_compare_dumps", "l2c_decoder_main", "l2c_decoder_run")
 
 
@@ -90,6 +93,12 @@ def load() -> ctypes.CDLL:
         "l2c_decoder_init_model": [p, p, p, i, i, p],
         "l2c_decoder_rmsnorm": [p, p, p, p, i, i, i, p],
         "l2c_decoder_softmax_argmax": [p, p, p, p, i, i, i, i, p],
+        "l2c_quantize_mxfp6": [p, p, p, i, i, p],
+        "l2c_nvfp4_tensor_scales": [p, p, p, p, ctypes.c_longlong, p, p],
+        "l2c_quantize_nvfp4": [p, p, p, p, p, i, i, p],
+        "l2c_to_bf16_x4": [p, p, ctypes.c_longlong, p],
+        "l2c_matmul_bf16": [p, p, p, p, i, i, i, p],
+        "l2c_matmul_mxfp6": [p, p, p, p, p, i, i, i, p],
     }
     for name, args in sigs.items():
         fn = getattr(lib, name)
@@ -310,3 +319,38 @@ def decoder(args, in_process: bool = False, timeout=None):
 
 def command_line(args) -> str:
     return " ".join(shlex.quote(a) for a in [HARNESS] + [str(a) for a in args])
+
+
+# ---------------------------------------------------------------------------
+# Low-precision classifier formats and contractions.
+
+def quantize_mxfp6(codes, scales, x, rows, width, stream=None):
+    _check(load().l2c_quantize_mxfp6(_vp(_ptr(codes)), _vp(_ptr(scales)), _vp(_ptr(x)), rows, width,
+                                     _vp(_stream(stream))), "l2c_quantize_mxfp6")
+
+
+def nvfp4_tensor_scales(tensor_scales, x, n, partials, alpha=None, other_decode=None, stream=None):
+    _check(load().l2c_nvfp4_tensor_scales(_vp(_ptr(tensor_scales)), _vp(_ptr(alpha)), _vp(_ptr(other_decode)),
+                                          _vp(_ptr(x)), n, _vp(_ptr(partials)), _vp(_stream(stream))),
+           "l2c_nvfp4_tensor_scales")
+
+
+def quantize_nvfp4(codes, scales, x, tensor_scales, rows, width, expanded=None, stream=None):
+    _check(load().l2c_quantize_nvfp4(_vp(_ptr(codes)), _vp(_ptr(scales)), _vp(_ptr(expanded)), _vp(_ptr(x)),
+                                     _vp(_ptr(tensor_scales)), rows, width, _vp(_stream(stream))),
+           "l2c_quantize_nvfp4")
+
+
+def to_bf16_x4(out, inp, n, stream=None):
+    _check(load().l2c_to_bf16_x4(_vp(_ptr(out)), _vp(_ptr(inp)), n, _vp(_stream(stream))), "l2c_to_bf16_x4")
+
+
+def matmul_bf16(out, X, W, batch, cols, rows, alpha=None, stream=None):
+    _check(load().l2c_matmul_bf16(_vp(_ptr(out)), _vp(_ptr(X)), _vp(_ptr(W)), _vp(_ptr(alpha)), batch, cols,
+                                  rows, _vp(_stream(stream))), "l2c_matmul_bf16")
+
+
+def matmul_mxfp6(out, X, Xscales, W, Wscales, batch, cols, rows, stream=None):
+    _check(load().l2c_matmul_mxfp6(_vp(_ptr(out)), _vp(_ptr(X)), _vp(_ptr(Xscales)), _vp(_ptr(W)),
+                                   _vp(_ptr(Wscales)), batch, cols, rows, _vp(_stream(stream))),
+           "l2c_matmul_mxfp6")

@@ -129,6 +129,57 @@ int l2c_quantize_fp8(uint8_t *codes, float *scales, const float *W, int rows, in
 int l2c_to_bf16(uint16_t *out, const float *in, size_t n, hipStream_t stream);
 
 /*
+ * Low-precision classifier formats (experiments/blackwell/lowprec/spec.json
+ * "formats", "rounding", "mxfp6", "nvfp4"; the reference's device quantizers
+ * are decoder_lowprec.cu:202-340 and its GEMMs CUTLASS calls at
+ * decoder_lowprec.cu:751-764). Every encoder rounds to nearest with ties to
+ * the even code, saturates, and writes +0 for magnitudes that round to zero.
+ *
+ * l2c_quantize_mxfp6: x [rows][width] (width % 32 == 0, x 16-byte aligned) to
+ *   E3M2 codes, a packed little-endian 6-bit stream per row (value i at bits
+ *   6i..6i+5, width * 3 / 4 bytes per row), and one UE8M0 scale byte per 32
+ *   values, scales[rows][width / 32]: X = floor(log2(block max)) - 4 clamped to
+ *   [-127, 127], code X + 127, elements E3M2(v * 2^-X); a zero block has scale 0
+ *   and codes 0. (The reference stores the scale bytes in CUTLASS's tile layout;
+ *   the values are the same.)
+ * l2c_nvfp4_tensor_scales: tensor_scales[0] = s = 2688 / max|x| (1 when the
+ *   maximum is 0), tensor_scales[1] = d = 1 / s, and, when alpha is not NULL,
+ *   *alpha = d * *other_decode, all FP32 on the device. partials: a device
+ *   workspace of L2C_NVFP4_PARTIALS floats. Two launches, no atomics, no memset.
+ * l2c_quantize_nvfp4: x [rows][width] (width % 16 == 0) to E2M1 codes (two per
+ *   byte, even index in the low nibble) and UE4M3 scales[rows][width / 16]:
+ *   scale code UE4M3((block max / 6) * s), codes E2M1((v * s) / f), f the scale's
+ *   value, FP32 operations in this order; a zero scale code zeroes the block.
+ *   s is read from tensor_scales[0] on the device. expanded_bf16 (optional,
+ *   [rows][width]) receives each element's exact value code * f as bf16.
+ * l2c_to_bf16_x4: l2c_to_bf16 for n % 4 == 0 and 16-byte aligned input.
+ */
+#define L2C_NVFP4_PARTIALS 1024
+int l2c_quantize_mxfp6(uint8_t *codes, uint8_t *scales, const float *x, int rows, int width,
+                       hipStream_t stream);
+int l2c_nvfp4_tensor_scales(float *tensor_scales, float *alpha, const float *other_decode,
+                            const float *x, long long n, float *partials, hipStream_t stream);
+int l2c_quantize_nvfp4(uint8_t *codes, uint8_t *scales, uint16_t *expanded_bf16, const float *x,
+                       const float *tensor_scales, int rows, int width, hipStream_t stream);
+int l2c_to_bf16_x4(uint16_t *out, const float *in, long long n, hipStream_t stream);
+
+/*
+ * Classifier contractions of the lowprec cases, out[b][r] = sum_k X[b][k] W[r][k]
+ * (X batch x cols, W rows x cols, out batch x rows, FP32 accumulation):
+ * l2c_matmul_bf16: bf16 X and W on the bf16 matrix cores (cols % 32 == 0); every
+ *   output is multiplied by *alpha when alpha (a device pointer) is not NULL.
+ *   The bf16 case (CUTLASS Sm80 GEMM, decoder_lowprec.cu:82-89) and, on the exact
+ *   bf16 expansions of NVFP4 operands with alpha = d_X * d_W, the NVFP4 case.
+ * l2c_matmul_mxfp6: MXFP6 X and W as l2c_quantize_mxfp6 writes them, on the
+ *   scaled matrix cores (cols % 128 == 0). The MXFP6 case (CUTLASS SM120
+ *   block-scaled GEMM, decoder_lowprec.cu:90-121).
+ */
+int l2c_matmul_bf16(float *out, const uint16_t *X, const uint16_t *W, const float *alpha, int batch,
+                    int cols, int rows, hipStream_t stream);
+int l2c_matmul_mxfp6(float *out, const uint8_t *X, const uint8_t *Xscales, const uint8_t *W,
+                     const uint8_t *Wscales, int batch, int cols, int rows, hipStream_t stream);
+
+/*
  * Batched greedy decoder (applications/loom_private/decoder): one step is
  *   l2c_decoder_rmsnorm -> l2c_matmul(logits, normalized, classifier) ->
  *   l2c_decoder_softmax_argmax

@@ -139,7 +139,7 @@ def crafted(rows=130, width=256, seed=5):
     m[2, :16] = e3
     m[2, 16:32] = [31.9, 31.0, 29.9, 28.1] + [1.0] * 12
     m[2, 32:64] = np.float32(e3 * 2) / np.float32(4.0)
-    for i in range(8):  # block maxima (2 - 2^-j) * 2^(i-4), then smaller values
+    for i in range(min(8, width // 32)):  # block maxima (2 - 2^-j) * 2^(i-4), then smaller values
         blk = m[3, 32 * i:32 * i + 32]
         blk[0] = np.float32((2.0 - 2.0 ** -(i + 2)) * 2.0 ** (i - 4))
         blk[1:] = np.float32(blk[0]) * np.linspace(-0.99, 0.98, 31, dtype=np.float32)
