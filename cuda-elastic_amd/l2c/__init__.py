@@ -25,6 +25,8 @@ LIB_PATH = os.path.join(LIB_DIR, "libl2c.so")
 HOST_LIB_PATH = os.path.join(LIB_DIR, "libl2c_host.so")
 HARNESS = os.path.join(BIN_DIR, "llama2c_hip")
 DECODER = os.path.join(BIN_DIR, "llama2c_decoder_hip")
+LOWPREC_CASES = ("fp32", "bf16", "mxfp6", "nvfp4")
+LOWPREC_DIR = os.path.join(BIN_DIR, "lowprec")
 COMPARE = os.path.join(BIN_DIR, "l2c_compare")
 
 RMS_EPSILON = 1.0e-5  # llama2c/llama2c_common.h:44
@@ -45,7 +47,9 @@ KERNEL_SYMBOLS = (
     "l2c_matmul_bf16", "l2c_matmul_mxfp6",
 )
 NVFP4_PARTIALS = 1024  # L2C_NVFP4_PARTIALS
-HOST_SYMBOLS = ("l2c_harness_main", "l2c_compare_dumps", "l2c_decoder_main", "l2c_decoder_run")
+HOST_SYMBOLS = ("l2c_harness_main", "l2c_compare_dumps", "l2c_decoder_main", "l2c_decoder_run",
+                "l2c_lowprec_main", "l2c_lowprec_run", "l2c_lowprec_host_quantize", "l2c_lowprec_fixture",
+                "l2c_lowprec_crafted")
 
 
 class L2CError(RuntimeError):
@@ -131,6 +135,18 @@ def load_host() -> ctypes.CDLL:
     host.l2c_decoder_main.restype = ctypes.c_int
     host.l2c_decoder_run.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_char_p)]
     host.l2c_decoder_run.restype = ctypes.c_int
+    host.l2c_lowprec_main.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p), ctypes.c_char_p,
+                                      ctypes.c_size_t]
+    host.l2c_lowprec_main.restype = ctypes.c_int
+    host.l2c_lowprec_run.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p)]
+    host.l2c_lowprec_run.restype = ctypes.c_int
+    vp = ctypes.c_void_p
+    host.l2c_lowprec_host_quantize.argtypes = [ctypes.c_int, vp, ctypes.c_int, ctypes.c_int, vp, vp, vp]
+    host.l2c_lowprec_host_quantize.restype = ctypes.c_int
+    host.l2c_lowprec_fixture.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
+    host.l2c_lowprec_fixture.restype = ctypes.c_int
+    host.l2c_lowprec_crafted.argtypes = [ctypes.c_int, ctypes.c_int, vp]
+    host.l2c_lowprec_crafted.restype = ctypes.c_int
     _host = host
     return host
 
@@ -315,6 +331,66 @@ def decoder(args, in_process: bool = False, timeout=None):
         if line.startswith("RESULT "):
             record = json.loads(line[len("RESULT "):])
     return proc.returncode, record, proc.stderr
+
+
+def lowprec(case, args, in_process: bool = False, timeout=None):
+    """Runs one case ("fp32", "bf16", "mxfp6", "nvfp4") of the lowprec
+    classifier experiment; returns (exit_code, record dict or None, stdout +
+    stderr text). args: the loom_private options, or ["--selftest"], or
+    ["--accuracy"]."""
+    import json
+    args = [str(a) for a in args]
+    index = LOWPREC_CASES.index(case)
+    if in_process:
+        host = load_host()
+        argv = [case.encode()] + [a.encode() for a in args]
+        arr = (ctypes.c_char_p * len(argv))(*argv)
+        buf = ctypes.create_string_buffer(1 << 20)
+        code = host.l2c_lowprec_main(index, len(argv), arr, buf, len(buf))
+        text = buf.value.decode()
+        return code, (json.loads(text) if text else None), ""
+    exe = os.path.join(LOWPREC_DIR, case)
+    if not os.path.exists(exe):
+        raise FileNotFoundError(f"{exe} is not built")
+    proc = subprocess.run([exe] + args, capture_output=True, text=True, timeout=timeout)
+    record = None
+    for line in proc.stdout.splitlines():
+        if line.startswith("RESULT "):
+            record = json.loads(line[len("RESULT "):])
+    return proc.returncode, record, proc.stdout + proc.stderr
+
+
+def lowprec_host_quantize(case, x, rows, width):
+    """The lowprec application's host reference quantizer (numpy in/out):
+    (codes uint16 [rows*width], scales uint8 [blocks], decode float)."""
+    import numpy as np
+    x = np.ascontiguousarray(x, np.float32)
+    codes = np.empty(rows * width, np.uint16)
+    block = {"bf16": 0, "mxfp6": 32, "nvfp4": 16}[case]
+    scales = np.empty(rows * width // block if block else 1, np.uint8)
+    decode = ctypes.c_float(0)
+    code = load_host().l2c_lowprec_host_quantize(LOWPREC_CASES.index(case), x.ctypes.data, rows, width,
+                                                 codes.ctypes.data, scales.ctypes.data, ctypes.addressof(decode))
+    if code:
+        raise L2CError(f"l2c_lowprec_host_quantize failed ({code})")
+    return codes, scales[: rows * width // block] if block else scales[:0], decode.value
+
+
+def lowprec_fixture(seed, width, vocab):
+    import numpy as np
+    emb = np.empty(width * vocab, np.float32)
+    cls = np.empty(width * vocab, np.float32)
+    if load_host().l2c_lowprec_fixture(seed, width, vocab, emb.ctypes.data, cls.ctypes.data):
+        raise L2CError("l2c_lowprec_fixture failed")
+    return emb.reshape(vocab, width), cls.reshape(vocab, width)
+
+
+def lowprec_crafted(rows, width):
+    import numpy as np
+    out = np.empty(rows * width, np.float32)
+    if load_host().l2c_lowprec_crafted(rows, width, out.ctypes.data):
+        raise L2CError("l2c_lowprec_crafted failed")
+    return out.reshape(rows, width)
 
 
 def command_line(args) -> str:

@@ -49,6 +49,35 @@ int l2c_compare_dumps(int count, const char *const *paths);
 int l2c_decoder_main(int argc, const char *const *argv, char *record, size_t capacity);
 int l2c_decoder_run(int argc, const char *const *argv);
 
+/*
+ * The lowprec classifier experiment (experiments/blackwell/lowprec): the
+ * decoder above with only its classifier replaced. lowprec_case selects the
+ * case the reference selects at compile time (decoder_lowprec.cu:1-35,
+ * -DLP_LOWPREC_CASE): 0 fp32, 1 bf16, 2 mxfp6, 3 nvfp4. argv is the command
+ * line of the reference's case binaries: the loom_private options of
+ * l2c_decoder_main (with --set fixture=0..3), or --selftest (the device
+ * quantizer against the host reference on crafted rows; exit 0 or 1), or
+ * --accuracy [--json-out PATH] (spec.json "accuracy"). Replaces main() of
+ * decoder_lowprec.cu:1414-1420.
+ *   l2c_lowprec_main writes the JSON record into record[0..capacity);
+ *   l2c_lowprec_run prints "RESULT <record>" to stdout instead.
+ */
+int l2c_lowprec_main(int lowprec_case, int argc, const char *const *argv, char *record, size_t capacity);
+int l2c_lowprec_run(int lowprec_case, int argc, const char *const *argv);
+
+/*
+ * The application's host reference, for tests: l2c_lowprec_host_quantize
+ * quantizes x [rows][width] as case lowprec_case (1..3) converts it, by table
+ * search (codes unpacked one per value, bf16 bits for case 1; scales one per
+ * block; *decode = the NVFP4 tensor decode scale); l2c_lowprec_fixture writes
+ * the dense fixture of spec.json "fixtures"; l2c_lowprec_crafted the self-test
+ * matrix. Return 0, or 2 for invalid arguments.
+ */
+int l2c_lowprec_host_quantize(int lowprec_case, const float *x, int rows, int width, unsigned short *codes,
+                              unsigned char *scales, float *decode);
+int l2c_lowprec_fixture(int seed, int width, int vocab, float *embedding, float *classifier);
+int l2c_lowprec_crafted(int rows, int width, float *out);
+
 #ifdef __cplusplus
 }
 #endif
