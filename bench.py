@@ -8,8 +8,9 @@ hipGraph, no copies: `value` is its microseconds per iteration (lower is
 better). The other benchmark configurations (decode GEMV 1 x 4096 x 11008,
 launch-bound 8 x 768 x 2048, the reference-compatible GEMV iteration at the
 large shape, the fused single launch, the MXFP4 / fp8 weights, and the
-loom-private llama2c decoder application at its large shape) and the
-graph/direct and copy/nocopy splits are reported under "lines".
+loom-private llama2c decoder application at its large shape, and the lowprec
+classifier experiment's fp32 / bf16 / MXFP6 / NVFP4 cases at that shape) and
+the graph/direct and copy/nocopy splits are reported under "lines".
 
 The harness runs in this process (libl2c_host.so via ctypes): HIP events on
 each operation's own stream time the kernels, so `roofline` comes from the
@@ -92,6 +93,36 @@ def decoder_line(l2c, mode, iterations=10, warmup=3):
             "application_us_per_invocation": app["batch_per_iteration_us"],
             "classifier_tflops_compute_scope": flops / (us * 1e-6) / 1e12,
             "note": "check-mode parity is a separate run (tests/test_decoder_gpu.py)"}
+
+
+# Graph application-scope µs per 4-step invocation of the reference's lowprec
+# cases on an RTX 5090 (experiments/blackwell/lowprec/README.md:134-139).
+LOWPREC_REFERENCE_US = {"fp32": 25285.8, "bf16": 6802.5, "mxfp6": 3816.6, "nvfp4": 1685.8}
+
+
+def lowprec_line(l2c, case, mode="graph", iterations=10, warmup=3):
+    """One case of the lowprec classifier experiment at its primary shape
+    (the decoder's large shape with the classifier replaced) under the
+    loom_private bench protocol, in-process."""
+    t = time.time()
+    code, rec, _ = l2c.lowprec(case, ["--action", "bench", "--launch", mode, "--iterations", iterations,
+                                      "--warmup", warmup], in_process=True)
+    if code != 0 or rec is None:
+        raise SystemExit(f"lowprec {case} bench failed (exit {code})")
+    comp, app = rec["timing"]["compute"], rec["timing"]["application"]
+    dims = rec["dimensions"]
+    flops = 2.0 * dims["classifier_macs_per_step"] * dims["steps"]
+    us = comp["batch_per_iteration_us"]
+    app_us = app["batch_per_iteration_us"]
+    log(f"[bench] lowprec {case} {mode}: application {app_us:.1f} us/invocation in {time.time() - t:.1f}s")
+    return {"name": f"lowprec_{case}_{mode}", "mode": mode, "case": case, "batch": dims["batch"],
+            "width": dims["width"], "vocab": dims["vocab"], "steps": dims["steps"],
+            "iterations": iterations, "warmup": warmup,
+            "compute_us_per_invocation": us, "application_us_per_invocation": app_us,
+            "classifier_flops_per_invocation": flops,
+            "reference_rtx5090_application_us": LOWPREC_REFERENCE_US[case],
+            "speedup_vs_reference": LOWPREC_REFERENCE_US[case] / app_us,
+            "note": "implementation check and accuracy are separate runs (tests/test_lowprec_app_gpu.py)"}
 
 
 def cpu_baseline(batch, size, rows, sample_vectors, sample_rows_norm):
@@ -180,6 +211,8 @@ def main():
             lines.append(summarize(name, run_line(l2c, a)))
         for mode in ("graph", "direct"):
             lines.append(decoder_line(l2c, mode))
+        for case in ("fp32", "bf16", "mxfp6", "nvfp4"):
+            lines.append(lowprec_line(l2c, case))
 
     gemm_us = headline["matmul_us"]
     flops = 2.0 * B * R * S

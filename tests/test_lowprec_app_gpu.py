@@ -97,6 +97,7 @@ def test_accuracy_matches_published(torch_gpu, l2c, case):
         d = ds[f"fixture{i}"]
         r = d["classifier_error"]["normalized_rms_error"]
         assert lo * 0.9 <= r <= hi * 1.1, (i, r)
-        # Accumulation order may move a near-tie; a token that differs then
-        # changes that sequence's later steps.
-        assert abs(d["tokens"]["agree"] - tokens) <= 6, (i, d["tokens"])
+        # Measured equal to the published counts. (A change of accumulation
+        # order could move a near-tie; a token that differs then changes that
+        # sequence's later steps.)
+        assert d["tokens"]["agree"] == tokens, (i, d["tokens"])
