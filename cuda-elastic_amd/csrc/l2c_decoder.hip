@@ -5,11 +5,14 @@
 // is l2c_matmul (gemm_f32_mfma_kernel); this file holds the model generator
 // and the two row kernels around it.
 //
-// Row kernels: one workgroup of 256 lanes per sequence, rows streamed with
-// 16-byte loads where the row is 16-byte aligned. Reductions are wave64
-// butterflies combined across the four waves in wave order, so every result
-// is deterministic (the decoder's check compares repeated invocations and
-// direct against graph launches bitwise).
+// Row kernels: one workgroup of 256 lanes per sequence. Rows up to 16384
+// values are register-resident: each lane loads its slice once (16-byte
+// loads where the row is 16-byte aligned), the reductions run on registers,
+// and the result is written once, so a row costs one read and one write of
+// HBM. Longer rows stream through the same lanes in passes. Reductions are
+// wave64 butterflies combined across the four waves in wave order, so every
+// result is deterministic (the decoder's check compares repeated
+// invocations and direct against graph launches bitwise).
 #include <climits>
 
 #include "l2c_common.h"
@@ -113,6 +116,175 @@ __global__ __launch_bounds__(kThreads) void decoder_rmsnorm_kernel(float *normal
   }
 }
 
+// Register-resident rmsnorm: lane t holds float4 chunks t + 256 c (VEC) or
+// values t + 256 i of the row, c < CHUNKS (4 * CHUNKS values a lane).
+template <int CHUNKS, bool VEC>
+__global__ __launch_bounds__(kThreads) void decoder_rmsnorm_regs_kernel(float *normalized, const int *tokens,
+                                                                        const float *embedding,
+                                                                        const float *weight, int width,
+                                                                        int vocab) {
+#pragma clang fp contract(off)
+  __shared__ float slots[kWaves];
+  const int sequence = blockIdx.x;
+  const int token = tokens[sequence];
+  float *o = normalized + static_cast<size_t>(sequence) * width;
+  const int t = threadIdx.x;
+  if (token < 0 || token >= vocab) {
+    for (int j = t; j < width; j += kThreads) o[j] = __builtin_nanf("");
+    return;
+  }
+  const float *x = embedding + static_cast<size_t>(token) * width;
+  float v[4 * CHUNKS];
+  if constexpr (VEC) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int i = t + c * kThreads;
+      const float4 q = i < width / 4 ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      v[4 * c] = q.x, v[4 * c + 1] = q.y, v[4 * c + 2] = q.z, v[4 * c + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4 * CHUNKS; ++i) {
+      const int j = t + i * kThreads;
+      v[i] = j < width ? x[j] : 0.0f;
+    }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4 * CHUNKS; ++i) ss += v[i] * v[i];
+  ss = group_sum(ss, slots);
+  ss /= static_cast<float>(width);
+  ss += 1e-5f;
+  const float scale = 1.0f / sqrtf(ss);
+  if constexpr (VEC) {
+    const float4 *w4 = reinterpret_cast<const float4 *>(weight);
+    float4 *o4 = reinterpret_cast<float4 *>(o);
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int i = t + c * kThreads;
+      if (i < width / 4) {
+        const float4 g = w4[i];
+        o4[i] = make_float4(g.x * (scale * v[4 * c]), g.y * (scale * v[4 * c + 1]), g.z * (scale * v[4 * c + 2]),
+                            g.w * (scale * v[4 * c + 3]));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4 * CHUNKS; ++i) {
+      const int j = t + i * kThreads;
+      if (j < width) o[j] = weight[j] * (scale * v[i]);
+    }
+  }
+}
+
+// (value, index) maximum over the workgroup with ties to the smaller index;
+// the result is valid in lane 0. INT_MAX marks "no candidate".
+__device__ __forceinline__ int group_argmax(float best, int best_index, float *vslots, int *islots) {
+#pragma unroll
+  for (int offset = L2C_WAVE / 2; offset > 0; offset >>= 1) {
+    const float ov = __shfl_xor(best, offset, L2C_WAVE);
+    const int oi = __shfl_xor(best_index, offset, L2C_WAVE);
+    if (ov > best || (ov == best && oi < best_index)) {
+      best = ov;
+      best_index = oi;
+    }
+  }
+  const int t = threadIdx.x;
+  if (t % L2C_WAVE == 0) {
+    vslots[t / L2C_WAVE] = best;
+    islots[t / L2C_WAVE] = best_index;
+  }
+  __syncthreads();
+  float v = vslots[0];
+  int i = islots[0];
+  for (int w = 1; w < kWaves; ++w) {
+    if (vslots[w] > v || (vslots[w] == v && islots[w] < i)) {
+      v = vslots[w];
+      i = islots[w];
+    }
+  }
+  return i;
+}
+
+// Register-resident softmax + argmax (same arithmetic as the streaming kernel
+// below): lane t holds chunks t + 256 c (VEC) or values t + 256 i, in
+// increasing index order, so a lane's first maximum is its smallest index.
+template <int CHUNKS, bool VEC>
+__global__ __launch_bounds__(kThreads) void decoder_softmax_argmax_regs_kernel(
+    float *probabilities, const float *logits, int *tokens, int *generated, int vocab, int steps, int step) {
+#pragma clang fp contract(off)
+  __shared__ float slots[3 * kWaves];
+  __shared__ int islots[kWaves];
+  const int sequence = blockIdx.x;
+  const float *x = logits + static_cast<size_t>(sequence) * vocab;
+  float *p = probabilities + static_cast<size_t>(sequence) * vocab;
+  const int t = threadIdx.x;
+  float v[4 * CHUNKS];
+  bool live[4 * CHUNKS];
+  if constexpr (VEC) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int i = t + c * kThreads;
+      const bool ok = i < vocab / 4;
+      const float4 q = ok ? x4[i] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      v[4 * c] = q.x, v[4 * c + 1] = q.y, v[4 * c + 2] = q.z, v[4 * c + 3] = q.w;
+      live[4 * c] = live[4 * c + 1] = live[4 * c + 2] = live[4 * c + 3] = ok;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4 * CHUNKS; ++i) {
+      const int r = t + i * kThreads;
+      live[i] = r < vocab;
+      v[i] = live[i] ? x[r] : -INFINITY;
+    }
+  }
+  float maximum = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4 * CHUNKS; ++i) maximum = fmaxf(maximum, v[i]);
+  maximum = group_max(maximum, slots);
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4 * CHUNKS; ++i) {
+    v[i] = live[i] ? expf(v[i] - maximum) : 0.0f;
+    sum += v[i];
+  }
+  sum = group_sum(sum, slots + kWaves);
+  float best = -INFINITY;
+  int best_index = INT_MAX;
+#pragma unroll
+  for (int i = 0; i < 4 * CHUNKS; ++i) {
+    const float q = v[i] / sum;
+    v[i] = q;
+    const int index = VEC ? 4 * (t + (i / 4) * kThreads) + i % 4 : t + i * kThreads;
+    if (live[i] && q > best) {
+      best = q;
+      best_index = index;
+    }
+  }
+  if constexpr (VEC) {
+    float4 *p4 = reinterpret_cast<float4 *>(p);
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int i = t + c * kThreads;
+      if (i < vocab / 4) p4[i] = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4 * CHUNKS; ++i) {
+      const int r = t + i * kThreads;
+      if (r < vocab) p[r] = v[i];
+    }
+  }
+  const int i = group_argmax(best, best_index, slots + 2 * kWaves, islots);
+  if (t == 0) {
+    const int next = i == INT_MAX ? -1 : i;
+    tokens[sequence] = next;
+    generated[static_cast<size_t>(sequence) * steps + step] = next;
+  }
+}
+
 // llama2.c softmax (max-subtracted expf divided by the float sum) followed by
 // sample_argmax (the first maximum of the probabilities), decoder.cu:127-198.
 // The argmax is the sequence's next token: written to tokens[sequence] for
@@ -197,6 +369,33 @@ extern "C" int l2c_decoder_init_model(float *embedding, float *classifier, float
   return hipSuccess;
 }
 
+// The smallest register-resident instance whose lanes hold n values, or
+// null for rows longer than 16384 (streamed instead).
+using RmsFn = void (*)(float *, const int *, const float *, const float *, int, int);
+using SoftFn = void (*)(float *, const float *, int *, int *, int, int, int);
+
+template <bool VEC>
+RmsFn rmsnorm_regs(int n) {
+  const int per_lane = (n + kThreads - 1) / kThreads;
+  if (per_lane <= 4) return decoder_rmsnorm_regs_kernel<1, VEC>;
+  if (per_lane <= 8) return decoder_rmsnorm_regs_kernel<2, VEC>;
+  if (per_lane <= 16) return decoder_rmsnorm_regs_kernel<4, VEC>;
+  if (per_lane <= 32) return decoder_rmsnorm_regs_kernel<8, VEC>;
+  if (per_lane <= 64) return decoder_rmsnorm_regs_kernel<16, VEC>;
+  return nullptr;
+}
+
+template <bool VEC>
+SoftFn softmax_regs(int n) {
+  const int per_lane = (n + kThreads - 1) / kThreads;
+  if (per_lane <= 4) return decoder_softmax_argmax_regs_kernel<1, VEC>;
+  if (per_lane <= 8) return decoder_softmax_argmax_regs_kernel<2, VEC>;
+  if (per_lane <= 16) return decoder_softmax_argmax_regs_kernel<4, VEC>;
+  if (per_lane <= 32) return decoder_softmax_argmax_regs_kernel<8, VEC>;
+  if (per_lane <= 64) return decoder_softmax_argmax_regs_kernel<16, VEC>;
+  return nullptr;
+}
+
 extern "C" int l2c_decoder_rmsnorm(float *normalized, const int *tokens, const float *embedding,
                                    const float *weight, int width, int vocab, int batch,
                                    hipStream_t stream) {
@@ -205,7 +404,10 @@ extern "C" int l2c_decoder_rmsnorm(float *normalized, const int *tokens, const f
   if (!normalized || !tokens || !embedding || !weight) return hipErrorInvalidValue;
   const bool vec = width % 4 == 0 && l2c_aligned16(normalized) && l2c_aligned16(embedding) &&
                    l2c_aligned16(weight);
-  if (vec)
+  if (const RmsFn regs = vec ? rmsnorm_regs<true>(width) : rmsnorm_regs<false>(width)) {
+    hipLaunchKernelGGL(regs, dim3(batch), dim3(kThreads), 0, stream, normalized, tokens, embedding, weight, width,
+                       vocab);
+  } else if (vec)
     hipLaunchKernelGGL(decoder_rmsnorm_kernel<true>, dim3(batch), dim3(kThreads), 0, stream,
                        normalized, tokens, embedding, weight, width, vocab);
   else
@@ -222,8 +424,13 @@ extern "C" int l2c_decoder_softmax_argmax(float *probabilities, const float *log
     return hipErrorInvalidValue;
   if (batch == 0) return hipSuccess;
   if (!probabilities || !logits || !tokens || !generated) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(decoder_softmax_argmax_kernel, dim3(batch), dim3(kThreads), 0, stream,
-                     probabilities, logits, tokens, generated, vocab, steps, step);
+  const bool vec = vocab % 4 == 0 && l2c_aligned16(probabilities) && l2c_aligned16(logits);
+  if (const SoftFn regs = vec ? softmax_regs<true>(vocab) : softmax_regs<false>(vocab))
+    hipLaunchKernelGGL(regs, dim3(batch), dim3(kThreads), 0, stream, probabilities, logits, tokens, generated, vocab,
+                       steps, step);
+  else
+    hipLaunchKernelGGL(decoder_softmax_argmax_kernel, dim3(batch), dim3(kThreads), 0, stream,
+                       probabilities, logits, tokens, generated, vocab, steps, step);
   L2C_LAUNCH_CHECK();
   return hipSuccess;
 }
