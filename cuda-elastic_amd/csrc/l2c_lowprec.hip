@@ -5,11 +5,14 @@
 // the reference's kernels are decoder_lowprec.cu:202-340).
 //
 // Layouts (row-major [rows][width], width along K):
-//  * MXFP6 codes: a little-endian bit stream per row, value i at bits
-//    6i..6i+5, so 32 values are 24 bytes and a row is width * 3 / 4 bytes.
-//    Scales: one byte per block, [rows][width / 32] (the reference stores
-//    them in CUTLASS's tile layout for its GEMM; the byte values are the
-//    same, and this layout is the one the MXFP6 GEMM here reads).
+//  * MXFP6: the tiled operand layout of the MXFP6 contraction (rows padded
+//    to Rp, a multiple of 32; padding rows hold zero codes and scales):
+//      codes  [width / 128][Rp / 32][4 blocks][32 rows][24 B]
+//      scales [width / 128][Rp][4 B]  (byte b = block b of the 128-value step)
+//    24 B are one 32-value block's E3M2 codes as a little-endian bit stream
+//    (value i at bits 6i..6i+5), the spec's packing; the reference keeps whole
+//    rows contiguous and its scales in CUTLASS's tile layout for its GEMM. The
+//    byte values are the same; only their order differs.
 //  * NVFP4 codes: two per byte, even index in the low nibble, [rows][width / 2].
 //    Scales: [rows][width / 16] UE4M3 bytes. Tensor scales: s = 2688 / a_t
 //    (1 when a_t = 0) and d = 1 / s, both FP32.
@@ -36,18 +39,29 @@ __device__ __forceinline__ float group_max(float v, int lanes) {
   return v;
 }
 
-// One group of 8 lanes per 32-value block; blocks are numbered row-major, so
-// block b covers x[32 b ..], codes[24 b ..] and scales[b].
+// One group of 8 lanes per 32-value block. Blocks are numbered in output
+// order, id = ((t * Rp / 32 + group) * 4 + b) * 32 + r for row 32 group + r and
+// block 4 t + b of the row, so block id's codes are bytes [24 id, 24 id + 24)
+// and a wave's groups write 192 contiguous bytes; each group reads its block's
+// 128 input bytes at once. Rows past `rows` are padding: zero codes and scale.
 __global__ __launch_bounds__(kThreads) void quantize_mxfp6_kernel(uint8_t *__restrict__ codes,
                                                                   uint8_t *__restrict__ scales,
-                                                                  const float *__restrict__ x,
-                                                                  long long blocks) {
+                                                                  const float *__restrict__ x, int rows,
+                                                                  int width, long long blocks) {
   const long long gid = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
   const long long blk = gid / 8;
   const int j = static_cast<int>(gid % 8);
+  const int Rp = (rows + 31) / 32 * 32;
+  const int r = static_cast<int>(blk % 32);
+  const int b = static_cast<int>((blk / 32) % 4);
+  const long long tg = blk / 128;  // t * (Rp / 32) + group
+  const int group = static_cast<int>(tg % (Rp / 32));
+  const long long t = tg / (Rp / 32);
+  const int row = group * 32 + r;
   const bool live = blk < blocks;
   float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if (live) v = reinterpret_cast<const float4 *>(x)[blk * 8 + j];
+  if (live && row < rows)
+    v = reinterpret_cast<const float4 *>(x + static_cast<size_t>(row) * width + (4 * t + b) * 32)[j];
   float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
   amax = group_max(amax, 8);
   const int X = l2c::mxfp6_exponent(amax);
@@ -66,7 +80,7 @@ __global__ __launch_bounds__(kThreads) void quantize_mxfp6_kernel(uint8_t *__res
   const unsigned phi = static_cast<unsigned>(__shfl(static_cast<int>(p), base + lo + 1, L2C_WAVE));
   const unsigned word = (plo >> off) | (phi << (24 - off));
   if (live && j < 6) reinterpret_cast<unsigned *>(codes + blk * 24)[j] = word;
-  if (live && j == 0) scales[blk] = amax > 0.0f ? static_cast<uint8_t>(X + 127) : 0;
+  if (live && j == 0) scales[(t * Rp + row) * 4 + b] = amax > 0.0f ? static_cast<uint8_t>(X + 127) : 0;
 }
 
 // Partial maxima of |x| over a grid-stride walk; one per workgroup.
@@ -178,14 +192,15 @@ bool grid_ok(long long threads, unsigned *grid) {
 
 extern "C" int l2c_quantize_mxfp6(uint8_t *codes, uint8_t *scales, const float *x, int rows, int width,
                                   hipStream_t stream) {
-  if (rows < 0 || width <= 0 || width % 32 != 0) return hipErrorInvalidValue;
+  if (rows < 0 || width <= 0 || width % 128 != 0) return hipErrorInvalidValue;
   if (rows == 0) return hipSuccess;
   if (!codes || !scales || !x || !l2c_aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 3u))
     return hipErrorInvalidValue;
-  const long long blocks = static_cast<long long>(rows) * (width / 32);
+  const long long blocks = static_cast<long long>((rows + 31) / 32 * 32) * (width / 32);
   unsigned grid;
   if (!grid_ok(blocks * 8, &grid)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(quantize_mxfp6_kernel, dim3(grid), dim3(kThreads), 0, stream, codes, scales, x, blocks);
+  hipLaunchKernelGGL(quantize_mxfp6_kernel, dim3(grid), dim3(kThreads), 0, stream, codes, scales, x, rows, width,
+                     blocks);
   L2C_LAUNCH_CHECK();
   return hipSuccess;
 }

@@ -110,8 +110,10 @@ int main(int argc, char **argv) {
       L2C(l2c_to_bf16_x4(xb, x, static_cast<long long>(vec), nullptr));
       L2C(l2c_to_bf16_x4(wb, m, static_cast<long long>(mat), nullptr));
     } else if (op == "mxfp6") {
-      CHECK(hipMalloc(&codes, mat * 3 / 4));
-      CHECK(hipMalloc(&sc8, mat / 32));
+      size_t cb = 0, sb = 0;
+      L2C(l2c_mxfp6_bytes(R, S, &cb, &sb));
+      CHECK(hipMalloc(&codes, cb));
+      CHECK(hipMalloc(&sc8, sb));
       L2C(l2c_quantize_mxfp6(xq, xs, x, B, S, nullptr));
       L2C(l2c_quantize_mxfp6(codes, sc8, m, R, S, nullptr));
     }

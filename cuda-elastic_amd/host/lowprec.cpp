@@ -315,8 +315,7 @@ class LowprecWorkload final : public lp::Workload {
       o.wide = device_array<uint16_t>(n);
     }
     if (c_ == kMxfp6) {
-      o.code_bytes = n / 4 * 3;
-      o.scale_bytes = n / 32;
+      LP_L2C(l2c_mxfp6_bytes(static_cast<int>(rows), static_cast<int>(d_.width), &o.code_bytes, &o.scale_bytes));
     } else if (c_ == kNvfp4) {
       o.code_bytes = n / 2;
       o.scale_bytes = n / 16;
@@ -362,19 +361,32 @@ class LowprecWorkload final : public lp::Workload {
       LP_HIP(hipMemcpy(q.codes.data(), o.wide.get(), n * 2, hipMemcpyDeviceToHost));
       return q;
     }
-    std::vector<uint8_t> bytes(o.code_bytes);
+    std::vector<uint8_t> bytes(o.code_bytes), scale_bytes(o.scale_bytes);
     LP_HIP(hipMemcpy(bytes.data(), o.codes.get(), o.code_bytes, hipMemcpyDeviceToHost));
-    q.scales.resize(o.scale_bytes);
-    LP_HIP(hipMemcpy(q.scales.data(), o.scales.get(), o.scale_bytes, hipMemcpyDeviceToHost));
-    const long long row_bytes = c_ == kMxfp6 ? d_.width / 4 * 3 : d_.width / 2;
-    l2c_host::parallel_ranges(static_cast<size_t>(o.rows), threads(), [&](size_t r0, size_t r1, size_t) {
-      for (long long r = static_cast<long long>(r0); r < static_cast<long long>(r1); ++r) {
-        const uint8_t *row = bytes.data() + r * row_bytes;
-        for (long long k = 0; k < d_.width; ++k)
-          q.codes[static_cast<size_t>(r * d_.width + k)] =
-              static_cast<uint16_t>(c_ == kMxfp6 ? unpack_e3m2(row, k) : unpack_e2m1(row, k));
-      }
-    });
+    LP_HIP(hipMemcpy(scale_bytes.data(), o.scales.get(), o.scale_bytes, hipMemcpyDeviceToHost));
+    const long long W = d_.width;
+    q.scales.resize(static_cast<size_t>(o.rows * (W / (c_ == kMxfp6 ? 32 : 16))));
+    if (c_ == kMxfp6) {
+      // Tiled operand layout: codes [W/128][Rp/32][4][32][24 B], scales [W/128][Rp][4].
+      const long long Rp = (o.rows + 31) / 32 * 32;
+      l2c_host::parallel_ranges(static_cast<size_t>(o.rows), threads(), [&](size_t r0, size_t r1, size_t) {
+        for (long long r = static_cast<long long>(r0); r < static_cast<long long>(r1); ++r)
+          for (long long kb = 0; kb < W / 32; ++kb) {
+            const long long t = kb / 4, b = kb % 4;
+            const uint8_t *block = bytes.data() + (((t * (Rp / 32) + r / 32) * 4 + b) * 32 + r % 32) * 24;
+            for (long long j = 0; j < 32; ++j)
+              q.codes[static_cast<size_t>(r * W + kb * 32 + j)] = static_cast<uint16_t>(unpack_e3m2(block, j));
+            q.scales[static_cast<size_t>(r * (W / 32) + kb)] = scale_bytes[static_cast<size_t>((t * Rp + r) * 4 + b)];
+          }
+      });
+    } else {
+      q.scales = scale_bytes;
+      l2c_host::parallel_ranges(static_cast<size_t>(o.rows), threads(), [&](size_t r0, size_t r1, size_t) {
+        for (long long r = static_cast<long long>(r0); r < static_cast<long long>(r1); ++r)
+          for (long long k = 0; k < W; ++k)
+            q.codes[static_cast<size_t>(r * W + k)] = static_cast<uint16_t>(unpack_e2m1(bytes.data() + r * (W / 2), k));
+      });
+    }
     if (c_ == kNvfp4) {
       float ts[2];
       LP_HIP(hipMemcpy(ts, o.tensor.get(), 8, hipMemcpyDeviceToHost));

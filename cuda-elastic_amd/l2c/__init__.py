@@ -44,7 +44,7 @@ KERNEL_SYMBOLS = (
     "l2c_strerror", "l2c_version",
     "l2c_decoder_init_model", "l2c_decoder_rmsnorm", "l2c_decoder_softmax_argmax",
     "l2c_quantize_mxfp6", "l2c_nvfp4_tensor_scales", "l2c_quantize_nvfp4", "l2c_to_bf16_x4",
-    "l2c_matmul_bf16", "l2c_matmul_mxfp6",
+    "l2c_matmul_bf16", "l2c_matmul_mxfp6", "l2c_mxfp6_bytes",
 )
 NVFP4_PARTIALS = 1024  # L2C_NVFP4_PARTIALS
 HOST_SYMBOLS = ("l2c_harness_main", "l2c_compare_dumps", "l2c_decoder_main", "l2c_decoder_run",
@@ -108,6 +108,8 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = ctypes.c_int
+    lib.l2c_mxfp6_bytes.argtypes = [i, i, ctypes.POINTER(sz), ctypes.POINTER(sz)]
+    lib.l2c_mxfp6_bytes.restype = ctypes.c_int
     lib.l2c_strerror.argtypes = [ctypes.c_int]
     lib.l2c_strerror.restype = ctypes.c_char_p
     lib.l2c_version.argtypes = []
@@ -399,6 +401,13 @@ def command_line(args) -> str:
 
 # ---------------------------------------------------------------------------
 # Low-precision classifier formats and contractions.
+
+def mxfp6_bytes(rows, width):
+    """(code bytes, scale bytes) of a [rows][width] MXFP6 operand in the tiled layout."""
+    c, s = ctypes.c_size_t(), ctypes.c_size_t()
+    _check(load().l2c_mxfp6_bytes(rows, width, ctypes.byref(c), ctypes.byref(s)), "l2c_mxfp6_bytes")
+    return c.value, s.value
+
 
 def quantize_mxfp6(codes, scales, x, rows, width, stream=None):
     _check(load().l2c_quantize_mxfp6(_vp(_ptr(codes)), _vp(_ptr(scales)), _vp(_ptr(x)), rows, width,

@@ -135,13 +135,16 @@ int l2c_to_bf16(uint16_t *out, const float *in, size_t n, hipStream_t stream);
  * decoder_lowprec.cu:751-764). Every encoder rounds to nearest with ties to
  * the even code, saturates, and writes +0 for magnitudes that round to zero.
  *
- * l2c_quantize_mxfp6: x [rows][width] (width % 32 == 0, x 16-byte aligned) to
- *   E3M2 codes, a packed little-endian 6-bit stream per row (value i at bits
- *   6i..6i+5, width * 3 / 4 bytes per row), and one UE8M0 scale byte per 32
- *   values, scales[rows][width / 32]: X = floor(log2(block max)) - 4 clamped to
- *   [-127, 127], code X + 127, elements E3M2(v * 2^-X); a zero block has scale 0
- *   and codes 0. (The reference stores the scale bytes in CUTLASS's tile layout;
- *   the values are the same.)
+ * l2c_quantize_mxfp6: x [rows][width] (width % 128 == 0, x 16-byte aligned) to
+ *   E3M2 codes and one UE8M0 scale byte per 32 values: X = floor(log2(block
+ *   max)) - 4 clamped to [-127, 127], scale code X + 127, elements E3M2(v * 2^-X);
+ *   a zero block has scale 0 and codes 0. Output in the tiled operand layout of
+ *   l2c_matmul_mxfp6, rows padded to Rp = 32 * ceil(rows / 32) (padding rows
+ *   zero): codes [width/128][Rp/32][4][32][24 B], where 24 B are one 32-value
+ *   block's codes as a little-endian 6-bit stream (value i at bits 6i..6i+5);
+ *   scales [width/128][Rp][4 B], byte b for block b of each 128-value step.
+ *   l2c_mxfp6_bytes gives both sizes. (The reference keeps rows contiguous and
+ *   its scale bytes in CUTLASS's tile layout; the byte values are the same.)
  * l2c_nvfp4_tensor_scales: tensor_scales[0] = s = 2688 / max|x| (1 when the
  *   maximum is 0), tensor_scales[1] = d = 1 / s, and, when alpha is not NULL,
  *   *alpha = d * *other_decode, all FP32 on the device. partials: a device
@@ -157,6 +160,7 @@ int l2c_to_bf16(uint16_t *out, const float *in, size_t n, hipStream_t stream);
 #define L2C_NVFP4_PARTIALS 1024
 int l2c_quantize_mxfp6(uint8_t *codes, uint8_t *scales, const float *x, int rows, int width,
                        hipStream_t stream);
+int l2c_mxfp6_bytes(int rows, int width, size_t *code_bytes, size_t *scale_bytes);
 int l2c_nvfp4_tensor_scales(float *tensor_scales, float *alpha, const float *other_decode,
                             const float *x, long long n, float *partials, hipStream_t stream);
 int l2c_quantize_nvfp4(uint8_t *codes, uint8_t *scales, uint16_t *expanded_bf16, const float *x,
@@ -170,9 +174,10 @@ int l2c_to_bf16_x4(uint16_t *out, const float *in, long long n, hipStream_t stre
  *   output is multiplied by *alpha when alpha (a device pointer) is not NULL.
  *   The bf16 case (CUTLASS Sm80 GEMM, decoder_lowprec.cu:82-89) and, on the exact
  *   bf16 expansions of NVFP4 operands with alpha = d_X * d_W, the NVFP4 case.
- * l2c_matmul_mxfp6: MXFP6 X and W as l2c_quantize_mxfp6 writes them, on the
- *   scaled matrix cores (cols % 128 == 0). The MXFP6 case (CUTLASS SM120
- *   block-scaled GEMM, decoder_lowprec.cu:90-121).
+ * l2c_matmul_mxfp6: MXFP6 X and W in the tiled layout l2c_quantize_mxfp6 writes,
+ *   on the scaled matrix cores (cols % 128 == 0, all four pointers 16-byte
+ *   aligned). The MXFP6 case (CUTLASS SM120 block-scaled GEMM,
+ *   decoder_lowprec.cu:90-121).
  */
 int l2c_matmul_bf16(float *out, const uint16_t *X, const uint16_t *W, const float *alpha, int batch,
                     int cols, int rows, hipStream_t stream);

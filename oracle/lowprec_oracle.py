@@ -81,6 +81,34 @@ def unpack_e3m2(packed, count):
     return (((p[byte] | (nxt << 8)) >> off) & 0x3F).astype(np.uint8)
 
 
+def tile_mxfp6(codes, scales, rows, width):
+    """Unpacked E3M2 codes [rows*width] and scale codes [rows*width/32] in the
+    tiled operand layout of the MXFP6 contraction (rows padded to Rp, a
+    multiple of 32, with zero codes and scales): code bytes
+    [width/128][Rp/32][4][32][24 B] (each 24 B the block's packed stream) and
+    scale bytes [width/128][Rp][4]."""
+    rp = (rows + 31) // 32 * 32
+    c = np.zeros((rp, width), np.uint8)
+    c[:rows] = np.asarray(codes, np.uint8).reshape(rows, width)
+    sc = np.zeros((rp, width // 32), np.uint8)
+    sc[:rows] = np.asarray(scales, np.uint8).reshape(rows, width // 32)
+    # [row][block][32] -> [t][group][b][r][32]
+    blocks = c.reshape(rp // 32, 32, width // 128, 4, 32).transpose(2, 0, 3, 1, 4)
+    packed = oracle.pack_e3m2(np.ascontiguousarray(blocks).ravel())
+    sbytes = np.ascontiguousarray(sc.reshape(rp, width // 128, 4).transpose(1, 0, 2)).ravel()
+    return packed, sbytes
+
+
+def untile_mxfp6(code_bytes, scale_bytes, rows, width):
+    """Inverse of tile_mxfp6: unpacked codes [rows*width], scales [rows*width/32]."""
+    rp = (rows + 31) // 32 * 32
+    n = rp * width
+    codes = unpack_e3m2(np.asarray(code_bytes, np.uint8)[: n * 3 // 4], n)
+    c = codes.reshape(width // 128, rp // 32, 4, 32, 32).transpose(1, 3, 0, 2, 4).reshape(rp, width)
+    s = np.asarray(scale_bytes, np.uint8)[: rp * width // 32].reshape(width // 128, rp, 4).transpose(1, 0, 2)
+    return np.ascontiguousarray(c[:rows]).ravel(), np.ascontiguousarray(s.reshape(rp, width // 32)[:rows]).ravel()
+
+
 def unpack_e2m1(packed, count):
     p = np.asarray(packed, np.uint8)
     i = np.arange(count)

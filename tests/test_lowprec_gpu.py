@@ -26,25 +26,37 @@ def inputs(name, rows, width):
     return (rng.standard_normal((rows, width)) * np.exp2(rng.integers(-30, 30, (rows, 1)))).astype(np.float32)
 
 
-CASES = [("crafted", 130, 256), ("crafted", 8, 128), ("fixture", 64, 1024), ("random", 1, 32 * 3),
+CASES = [("crafted", 130, 256), ("crafted", 8, 128), ("fixture", 64, 1024), ("random", 1, 128 * 3),
          ("random", 333, 2048)]
+
+
+def mxfp6_buffers(torch, l2c, rows, width):
+    cb, sb = l2c.mxfp6_bytes(rows, width)
+    assert cb == (rows + 31) // 32 * 32 * width * 3 // 4 and sb == (rows + 31) // 32 * 32 * width // 32
+    return (torch.full((cb,), 0xAB, dtype=torch.uint8, device="cuda"),
+            torch.full((sb,), 0xAB, dtype=torch.uint8, device="cuda"))
 
 
 @pytest.mark.parametrize("name,rows,width", CASES)
 def test_quantize_mxfp6_exact(torch_gpu, l2c, name, rows, width):
+    """Codes and scales bit for bit in the tiled operand layout, padding rows zero."""
     torch = torch_gpu
     print(f"case quantize_mxfp6 {name} {rows}x{width}", flush=True)
     x = inputs(name, rows, width)
-    codes = torch.full((rows * width * 3 // 4,), 0xAB, dtype=torch.uint8, device="cuda")
-    scales = torch.full((rows * width // 32,), 0xAB, dtype=torch.uint8, device="cuda")
+    codes, scales = mxfp6_buffers(torch, l2c, rows, width)
     l2c.quantize_mxfp6(codes, scales, dev(torch, x), rows, width)
     torch.cuda.synchronize()
     c, s = oracle.quantize_mxfp6(x, rows, width)
-    np.testing.assert_array_equal(codes.cpu().numpy(), oracle.pack_e3m2(c))
-    np.testing.assert_array_equal(scales.cpu().numpy(), s)
+    pc, ps = lo.tile_mxfp6(c, s, rows, width)
+    np.testing.assert_array_equal(codes.cpu().numpy(), pc)
+    np.testing.assert_array_equal(scales.cpu().numpy(), ps)
 
 
-@pytest.mark.parametrize("name,rows,width", CASES + [("random", 3, 16)])
+NVFP4_CASES = [("crafted", 130, 256), ("crafted", 8, 128), ("fixture", 64, 1024), ("random", 1, 32 * 3),
+               ("random", 333, 2048), ("random", 3, 16)]
+
+
+@pytest.mark.parametrize("name,rows,width", NVFP4_CASES)
 def test_quantize_nvfp4_exact(torch_gpu, l2c, name, rows, width):
     torch = torch_gpu
     print(f"case quantize_nvfp4 {name} {rows}x{width}", flush=True)
@@ -139,15 +151,13 @@ def test_matmul_mxfp6_bound(torch_gpu, l2c, batch, cols, rows):
     A = lo.dequantize_mxfp6(xc, xs, batch, cols)
     W = lo.dequantize_mxfp6(wc, ws, rows, cols)
     out = torch.full((batch, rows), np.nan, dtype=torch.float32, device="cuda")
-    l2c.matmul_mxfp6(out, dev(torch, oracle.pack_e3m2(xc)), dev(torch, xs), dev(torch, oracle.pack_e3m2(wc)),
-                     dev(torch, ws), batch, cols, rows)
+    txc, txs = lo.tile_mxfp6(xc, xs, batch, cols)
+    twc, tws = lo.tile_mxfp6(wc, ws, rows, cols)
+    l2c.matmul_mxfp6(out, dev(torch, txc), dev(torch, txs), dev(torch, twc), dev(torch, tws), batch, cols, rows)
     torch.cuda.synchronize()
     check_bound(out.cpu().numpy(), A, W, 1.0, cols)
-    u8 = torch.uint8
-    dxc = torch.empty(batch * cols * 3 // 4, dtype=u8, device="cuda")
-    dxs = torch.empty(batch * cols // 32, dtype=u8, device="cuda")
-    dwc = torch.empty(rows * cols * 3 // 4, dtype=u8, device="cuda")
-    dws = torch.empty(rows * cols // 32, dtype=u8, device="cuda")
+    dxc, dxs = mxfp6_buffers(torch, l2c, batch, cols)
+    dwc, dws = mxfp6_buffers(torch, l2c, rows, cols)
     l2c.quantize_mxfp6(dxc, dxs, dev(torch, x), batch, cols)
     l2c.quantize_mxfp6(dwc, dws, dev(torch, w), rows, cols)
     out2 = torch.full((batch, rows), np.nan, dtype=torch.float32, device="cuda")
