@@ -83,3 +83,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uin
 static inline bool l2c_aligned16(const void *p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
+
+// The quantized-weight kernel's bf16 form (l2c_qgemm.hip), for contractions
+// whose K is not a multiple of 64.
+int l2c_matmul_bf16_split(float *out, const uint16_t *X, const uint16_t *W, const float *alpha, int batch, int cols,
+                          int rows, hipStream_t stream);

@@ -32,9 +32,11 @@
 //    and waited (vmcnt) before the barrier of step t - 1.
 //  * Fragments: 3 x ds_read_b64 per operand. 32 lanes with consecutive rows
 //    read 24-byte-strided data: 32 distinct even bank pairs, conflict free.
-//  * Rows past M or N: their slab bytes are other in-bounds bytes of the
-//    operand or, past the buffer's end, zeros (buffer loads return 0 out of
-//    range); those rows are computed and never stored. K % 128 == 0.
+//  * Every access is in bounds by construction (no reliance on buffer range
+//    checks): a tile's row groups past the operand's padded rows re-read its
+//    last group (a wave-uniform clamp), and scale-word lanes past the padded
+//    rows re-read its last four rows (a per-lane clamp). Those rows are
+//    computed and never stored. K % 128 == 0.
 //  * Workgroup order is remapped per XCD as in the other contractions.
 #include "l2c_common.h"
 #include "../../include/l2c.h"
@@ -88,6 +90,14 @@ __global__ __launch_bounds__(kThreads, 1) void mxfp6_gemm_kernel(float *__restri
   const __amdgpu_buffer_rsrc_t rxs = l2c::buffer_rsrc(Xs, static_cast<uint32_t>(Mp) * 4 * steps);
   const __amdgpu_buffer_rsrc_t rws = l2c::buffer_rsrc(Ws, static_cast<uint32_t>(Np) * 4 * steps);
   const int lane16 = 16 * lane;
+  // Slab KB d of a tile lies in its row group d / 3; groups past the padded
+  // rows are replaced by the last one.
+  const int xlast = Mp / 32 - 1 - m0 / 32, wlast = Np / 32 - 1 - n0 / 32;
+  auto slab = [](int d, int glast) __attribute__((always_inline)) {
+    return min(d / 3, glast) * kGroup + (d % 3) * 1024;
+  };
+  // Scale words: lane covers rows 4 lane .. 4 lane + 3 of the tile.
+  const int xsl = min(lane16, (Mp - m0) * 4 - 16), wsl = min(lane16, (Np - n0) * 4 - 16);
 
   auto dma = [&](int stage, int t) __attribute__((always_inline)) {
     unsigned char *base = lds + stage * kStage;
@@ -95,16 +105,16 @@ __global__ __launch_bounds__(kThreads, 1) void mxfp6_gemm_kernel(float *__restri
 #pragma unroll
     for (int k = 0; k < 3; ++k)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr *)(base + (8 * k + wave) * 1024), 16, lane16,
-                                               xs0 + (8 * k + wave) * 1024, 0, 0);
+                                               xs0 + slab(8 * k + wave, xlast), 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + kXBytes + wave * 1024), 16, lane16,
-                                             ws0 + wave * 1024, 0, 0);
+                                             ws0 + slab(wave, wlast), 0, 0);
     if (wave < 4)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + kXBytes + (8 + wave) * 1024), 16, lane16,
-                                               ws0 + (8 + wave) * 1024, 0, 0);
+                                               ws0 + slab(8 + wave, wlast), 0, 0);
     else if (wave == 4)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rxs, (lds_ptr *)(base + kXS), 16, lane16, Mp * 4 * t + m0 * 4, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rxs, (lds_ptr *)(base + kXS), 16, xsl, Mp * 4 * t + m0 * 4, 0, 0);
     else if (wave == 5)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rws, (lds_ptr *)(base + kWS), 16, lane16, Np * 4 * t + n0 * 4, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rws, (lds_ptr *)(base + kWS), 16, wsl, Np * 4 * t + n0 * 4, 0, 0);
   };
   // Waits for this wave's DMA of the older of two outstanding steps (waves
   // 0..5 issue 5 instructions a step, 6 and 7 issue 4) and its LDS reads, then

@@ -473,8 +473,10 @@ extern "C" int l2c_to_bf16(uint16_t *out, const float *in, size_t n, hipStream_t
   return hipSuccess;
 }
 
-extern "C" int l2c_matmul_bf16(float *out, const uint16_t *X, const uint16_t *W, const float *alpha, int batch,
-                               int cols, int rows, hipStream_t stream) {
+// bf16 weights through this kernel: l2c_matmul_bf16 (l2c_bfgemm.hip) uses it for
+// K % 64 == 32, which its own kernel does not take.
+int l2c_matmul_bf16_split(float *out, const uint16_t *X, const uint16_t *W, const float *alpha, int batch, int cols,
+                          int rows, hipStream_t stream) {
   if (batch < 0 || cols <= 0 || rows < 0 || cols % 32 != 0) return hipErrorInvalidValue;
   if (batch == 0 || rows == 0) return hipSuccess;
   if (!out || !X || !W || !l2c_aligned16(X) || !l2c_aligned16(W)) return hipErrorInvalidValue;
