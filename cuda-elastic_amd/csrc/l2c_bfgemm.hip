@@ -103,17 +103,16 @@ __global__ __launch_bounds__(kThreads, 1) void bf16_gemm_kernel(float *__restric
   const int a0 = (wm * 128 + r) * 128, b0 = kXBytes + (wn * 64 + r) * 128;
   const int c0 = 16 * ((4 * h + 2 * g) ^ sw), c1 = 16 * ((4 * h + 2 * g + 1) ^ sw);
   u32x4 fa[4][2], fb[2][2];
+  // Chunk 0's six reads, then chunk 1's, in the order the main loop uses.
   auto read = [&](int stage) __attribute__((always_inline)) {
     const unsigned char *base = lds + stage * kStage;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      fa[i][0] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c0);
-      fa[i][1] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c1);
-    }
+    for (int q = 0; q < 2; ++q) {
+      const int c = q ? c1 : c0;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      fb[j][0] = *reinterpret_cast<const u32x4 *>(base + b0 + 4096 * j + c0);
-      fb[j][1] = *reinterpret_cast<const u32x4 *>(base + b0 + 4096 * j + c1);
+      for (int i = 0; i < 4; ++i) fa[i][q] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) fb[j][q] = *reinterpret_cast<const u32x4 *>(base + b0 + 4096 * j + c);
     }
   };
   f32x16 acc[4][2];
@@ -123,31 +122,63 @@ __global__ __launch_bounds__(kThreads, 1) void bf16_gemm_kernel(float *__restric
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-  auto mma = [&]() __attribute__((always_inline)) {
+  // MFMAs of the wave's k-chunk q (8 per step).
+  auto mma = [&](int q) __attribute__((always_inline)) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i][q]),
-                                                              __builtin_bit_cast(bf16x8, fb[j][q]), acc[i][j], 0, 0, 0);
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i][q]),
+                                                            __builtin_bit_cast(bf16x8, fb[j][q]), acc[i][j], 0, 0, 0);
   };
 
+  // Step t: chunk-0 MFMAs of F(t); barrier (DMA(t + 1) landed, every wave's
+  // reads of F(t) from stage t % 3 done); DMA(t + 3) into stage t % 3; chunk-1
+  // MFMAs of F(t) interleaved with the reads of F(t + 1): chunk 0's registers
+  // are free at once, each chunk-1 register right after its last MFMA. LDS and
+  // the matrix cores then work at the same time; DMA keeps two steps to land.
   const int total = K / 64;
   const int last = total - 1;
   dma(0, 0);
   dma(1, min(1, last));
-  sync();
+  sync();  // step 0 landed
+  dma(2, min(2, last));
   read(0);
+  __builtin_amdgcn_sched_barrier(0);
   int cur = 0;
   for (int t = 0; t < total; ++t) {
     const int nxt = cur == kStages - 1 ? 0 : cur + 1;
-    const int far = nxt == kStages - 1 ? 0 : nxt + 1;
-    dma(far, min(t + 2, last));
-    mma();
+    mma(0);
     sync();
-    read(nxt);
+    dma(cur, min(t + 3, last));
+    const unsigned char *base = lds + nxt * kStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[i][0] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) fb[j][0] = *reinterpret_cast<const u32x4 *>(base + b0 + 4096 * j + c0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i][1]),
+                                                            __builtin_bit_cast(bf16x8, fb[j][1]), acc[i][j], 0, 0, 0);
+      fa[i][1] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c1);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) fb[j][1] = *reinterpret_cast<const u32x4 *>(base + b0 + 4096 * j + c1);
+    // Order of the region after the barrier: the six DMA instructions and the
+    // six chunk-0 reads first, then MFMA pairs each followed by one read.
+    __builtin_amdgcn_sched_group_barrier(0x020, 6, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    // Keep the reads of F(t + 1) in this step: the next step's chunk-0 MFMAs
+    // must find them already in flight.
+    __builtin_amdgcn_sched_barrier(0);
     cur = nxt;
   }
 

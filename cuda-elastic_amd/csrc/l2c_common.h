@@ -88,3 +88,10 @@ static inline bool l2c_aligned16(const void *p) {
 // whose K is not a multiple of 64.
 int l2c_matmul_bf16_split(float *out, const uint16_t *X, const uint16_t *W, const float *alpha, int batch, int cols,
                           int rows, hipStream_t stream);
+// The quantized-weight contraction for cols % 64 == 0 (l2c_qgemm_ks.hip),
+// called by l2c_matmul_q after its argument checks.
+int l2c_matmul_q_ks(float *out, const uint16_t *X, const uint8_t *Wq, const void *scales, int fmt, int batch,
+                    int cols, int rows, hipStream_t stream);
+// Workgroups of that kernel resident per CU (its grid and block are those of
+// the l2c_qgemm.hip kernel: one 512-lane workgroup per 256 x 128 tile).
+int l2c_qgemm_ks_occupancy(int fmt, int *blocks_per_cu);

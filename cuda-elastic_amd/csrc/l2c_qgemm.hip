@@ -405,10 +405,10 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
 
 int l2c_qgemm_launch_shape(int fmt, int batch, int cols, int rows, int *grid, int *block,
                            int *blocks_per_cu) {
-  (void)cols;
   if (fmt != L2C_Q_MXFP4 && fmt != L2C_Q_FP8) return hipErrorInvalidValue;
   *grid = ((batch + kBM - 1) / kBM) * ((rows + kBN - 1) / kBN);
   *block = kThreads;
+  if (cols % 64 == 0) return l2c_qgemm_ks_occupancy(fmt, blocks_per_cu);
   const void *fn = fmt == L2C_Q_MXFP4 ? reinterpret_cast<const void *>(qgemm_kernel<L2C_Q_MXFP4>)
                                       : reinterpret_cast<const void *>(qgemm_kernel<L2C_Q_FP8>);
   return static_cast<int>(hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, kThreads, 0));
@@ -428,6 +428,8 @@ extern "C" int l2c_matmul_q(float *out, const void *Xbf16, const void *Wq, const
   const dim3 grid(static_cast<unsigned>(tiles)), block(kThreads);
   const uint16_t *X = static_cast<const uint16_t *>(Xbf16);
   const uint8_t *W = static_cast<const uint8_t *>(Wq);
+  if (cols % 64 == 0 && (fmt == L2C_Q_FP8 || (reinterpret_cast<uintptr_t>(scales) & 1u) == 0))
+    return l2c_matmul_q_ks(out, X, W, scales, fmt, batch, cols, rows, stream);
   if (fmt == L2C_Q_MXFP4)
     hipLaunchKernelGGL(qgemm_kernel<L2C_Q_MXFP4>, grid, block, 0, stream, out, X, W, scales, batch,
                        rows, cols);

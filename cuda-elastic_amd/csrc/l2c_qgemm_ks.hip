@@ -1,0 +1,308 @@
+// Quantized-weight contraction out[b][r] = sum_k X[b][k] * deq(W)[r][k] for
+// K % 64 == 0: bf16 activations, MXFP4 (E2M1 codes, one E8M0 scale per 32 k)
+// or per-row-scaled fp8 E4M3 weights, in the layouts l2c_quantize_mxfp4 and
+// l2c_quantize_fp8 write (codes row-major, MXFP4 scales [rows][K/32]).
+// l2c_matmul_q routes K % 64 == 32 to the kernel in l2c_qgemm.hip.
+//
+// Kernel design (the structure of the bf16 contraction in l2c_bfgemm.hip):
+//  * The product runs on the bf16 matrix cores (v_mfma_f32_32x32x16_bf16);
+//    the weight codes are converted exactly to bf16 in registers by the
+//    gfx950 scaled conversions (v_cvt_scalef32_pk_bf16_fp4 / _fp8), an E2M1
+//    value times 2^(s - 127) or an E4M3 value having at most 4 significant
+//    bits. The fp8 row scale multiplies each output in the epilogue.
+//  * Tile 256 (batch) x 128 (rows) x 64 (k per step), 8 wavefronts in k-slice
+//    pairs: waves w and w + 4 share a SIMD and a 128 x 64 output sub-tile and
+//    take the step's k-chunks 2g, 2g + 1 (g = w / 4); lane (r, h) of MFMA q
+//    supplies k = 32h + 8q + 0..7 for both operands, so a lane's codes for its
+//    two chunks are 8 contiguous bytes (MXFP4, one scale block h) or 16 (fp8).
+//    The pairs' partial sums are added once at the end through LDS.
+//  * LDS DMA staging (buffer_load ... lds): X 32 KB a step as 32 1-KB
+//    instructions (4 a wave); W codes 4 KB (MXFP4, waves 0-3) or 8 KB (fp8,
+//    one a wave); MXFP4 scales as 2-byte DMAs, one row a lane (waves 4, 5),
+//    each landing zero-extended in its own LDS word (a 2-byte DMA writes
+//    lane i's bytes at word i). The weight bytes a step are a quarter (MXFP4)
+//    or half (fp8) of the bf16 weights'.
+//  * Bounds, measured at 1024 x 16384 x 8192: the L2-to-LDS staging rate of
+//    this tiling (about 17 TB/s with the X re-reads across XCDs) and the bf16
+//    matrix cores' rate on random operands (about 1.7 PFLOP/s, against 2.4
+//    on constant data: a power limit). The MXFP4 conversions run on the VALU
+//    beside the other wave's MFMAs.
+//  * 16-byte chunks of LDS rows are XOR-swizzled by row bits (X: bits 1..3;
+//    W: bit 3 for 32-byte MXFP4 rows, bits 2..3 for 64-byte fp8 rows), applied
+//    on the DMA's source side, so the fragment reads avoid bank conflicts
+//    (MXFP4's 8-byte reads keep a two-way conflict on 2 KB a wave and step).
+//  * Three stages, one barrier a step: the chunk-0 MFMAs of step t, the
+//    barrier (DMA of step t + 1 landed, every wave's reads of step t done),
+//    the DMA of step t + 3 into the freed stage, then the chunk-1 MFMAs
+//    interleaved with the reads of step t + 1.
+//  * Every access is in bounds by construction: rows past the operand are
+//    clamped per lane to its last row; those rows are never stored.
+#include "l2c_common.h"
+#include "../../include/l2c.h"
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_ptr;
+
+constexpr int kBM = 256;
+constexpr int kBN = 128;
+constexpr int kThreads = 512;
+constexpr int kStages = 3;
+constexpr int kXcds = 8;
+constexpr int kXBytes = kBM * 128;    // 256 rows x 64 bf16
+constexpr int kExchange = 131072;     // 4 sub-tiles x 8 blocks x 16 values x 64 lanes x 4 B
+
+template <int FMT>
+struct Layout {
+  static constexpr bool kMx = FMT == L2C_Q_MXFP4;
+  static constexpr int kWRow = kMx ? 32 : 64;  // code bytes per W row and step
+  static constexpr int kLanesPerRow = kWRow / 16;
+  static constexpr int kSOff = kXBytes + kBN * kWRow;
+  static constexpr int kStage = kSOff + (kMx ? kBN * 4 : 0);
+  static constexpr int kLds = kStages * kStage > kExchange ? kStages * kStage : kExchange;
+  static __device__ __forceinline__ int wswizzle(int row) { return kMx ? (row >> 3) & 1 : (row >> 2) & 3; }
+};
+
+__device__ __forceinline__ int xswizzle(int row) { return (row >> 1) & 7; }
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict__ out,
+                                                               const uint16_t *__restrict__ X,
+                                                               const uint8_t *__restrict__ Wq,
+                                                               const void *__restrict__ scales, int M, int N,
+                                                               int K) {
+  using L = Layout<FMT>;
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[L::kLds];
+  int tile = blockIdx.x;
+  const int tiles = gridDim.x;
+  if (tiles % kXcds == 0) tile = (tile % kXcds) * (tiles / kXcds) + tile / kXcds;
+  const int mtiles = (M + kBM - 1) / kBM;
+  const int m0 = (tile % mtiles) * kBM, n0 = (tile / mtiles) * kBN;
+  const int mrows = min(kBM, M - m0), nrows = min(kBN, N - n0);
+  const int tid = threadIdx.x, lane = tid % L2C_WAVE;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / L2C_WAVE);
+  const int g = wave >> 2, p = wave & 3;
+  const int wm = p & 1, wn = p >> 1;
+  const int r = lane % 32, h = lane / 32;
+  const int xrb = 2 * K;                  // X bytes per row
+  const int wrb = L::kMx ? K / 2 : K;     // code bytes per W row
+  const int srb = K / 32;                 // MXFP4 scale bytes per row
+  const __amdgpu_buffer_rsrc_t rx =
+      l2c::buffer_rsrc(X + static_cast<size_t>(m0) * K, static_cast<uint32_t>(mrows) * xrb);
+  const __amdgpu_buffer_rsrc_t rw =
+      l2c::buffer_rsrc(Wq + static_cast<size_t>(n0) * wrb, static_cast<uint32_t>(nrows) * wrb);
+  const __amdgpu_buffer_rsrc_t rs =
+      L::kMx ? l2c::buffer_rsrc(static_cast<const uint8_t *>(scales) + static_cast<size_t>(n0) * srb,
+                                static_cast<uint32_t>(nrows) * srb)
+             : rw;
+
+  // DMA sources (per-lane parts; the step's k offset is scalar). X: block b of
+  // 8 rows (b = 8k + wave), lane i fills row 8b + i / 8, slot i % 8 with chunk
+  // (i % 8) ^ xswizzle(row). W: wave w fills rows (64 / lanes-per-row) w + i /
+  // lanes-per-row, slot i % lanes-per-row. Scales: wave 4 + s fills row 64 s + i.
+  const int lrow = 8 * wave + lane / 8;
+  const int lchunk = 16 * ((lane % 8) ^ xswizzle(lrow));
+  int xsrc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) xsrc[k] = min(64 * k + lrow, mrows - 1) * xrb + lchunk;
+  const int wrow = (64 / L::kLanesPerRow) * wave + lane / L::kLanesPerRow;
+  const int wsrc = min(wrow, nrows - 1) * wrb + 16 * ((lane % L::kLanesPerRow) ^ L::wswizzle(wrow));
+  const int ssrc = min(max(64 * (wave - 4) + lane, 0), nrows - 1) * srb;
+
+  auto dma = [&](int stage, int t) __attribute__((always_inline)) {
+    unsigned char *base = lds + stage * L::kStage;
+    if constexpr (L::kMx) {
+      if (wave < 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + kXBytes + wave * 1024), 16, wsrc, 32 * t, 0,
+                                                 0);
+      else if (wave < 6)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr *)(base + L::kSOff + (wave - 4) * 256), 2, ssrc, 2 * t,
+                                                 0, 0);
+    } else {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + kXBytes + wave * 1024), 16, wsrc, 64 * t, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr *)(base + (8 * k + wave) * 1024), 16, xsrc[k], 128 * t,
+                                               0, 0);
+  };
+  // Waits for this wave's DMA of the older of two outstanding steps and its
+  // LDS reads, then the workgroup barrier. DMA instructions a step: 5 (fp8;
+  // MXFP4 waves 0..5), 4 (MXFP4 waves 6, 7).
+  auto sync = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (!L::kMx || wave < 6)
+      asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Fragments. X rows wm * 128 + 32 i + r, chunks 4h + 2g (+1). W rows
+  // wn * 64 + 32 j + r (the swizzle of row + 32 equals that of row): MXFP4
+  // bytes 16h + 8g of the 32-byte row (chunk h), fp8 bytes 32h + 16g (chunk
+  // 2h + g); MXFP4 scale word of the row, byte h.
+  const int xsw = xswizzle(r);
+  const int a0 = (wm * 128 + r) * 128;
+  const int c0 = 16 * ((4 * h + 2 * g) ^ xsw), c1 = 16 * ((4 * h + 2 * g + 1) ^ xsw);
+  const int wr0 = wn * 64 + r;
+  const int wb = L::kMx ? kXBytes + wr0 * 32 + 16 * (h ^ L::wswizzle(wr0)) + 8 * g
+                        : kXBytes + wr0 * 64 + 16 * ((2 * h + g) ^ L::wswizzle(wr0));
+  const int sb = L::kSOff + 4 * wr0;
+  u32x4 fa[4][2];
+  u32x4 wc[2];  // MXFP4 uses the low two words
+  uint32_t ws[2];
+  // Codes (and the MXFP4 scale byte h, in the low byte of ws) of a stage.
+  auto read_w = [&](const unsigned char *base) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if constexpr (L::kMx) {
+        const u32x2 v = *reinterpret_cast<const u32x2 *>(base + wb + 1024 * j);
+        wc[j][0] = v[0], wc[j][1] = v[1];
+        ws[j] = *reinterpret_cast<const uint32_t *>(base + sb + 128 * j) >> (8 * h);
+      } else {
+        wc[j] = *reinterpret_cast<const u32x4 *>(base + wb + 2048 * j);
+      }
+    }
+  };
+  auto read = [&](int stage) __attribute__((always_inline)) {
+    const unsigned char *base = lds + stage * L::kStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[i][0] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c0);
+    read_w(base);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[i][1] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c1);
+  };
+  // B operands of the wave's two chunks from the codes: 8 k a chunk, two per
+  // conversion.
+  bf16x8 b[2][2];
+  auto convert = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        uint32_t d[4];
+        if constexpr (L::kMx) {
+          // Block scale 2^(e - 127) as fp32 (e = 0 is the subnormal 2^-127).
+          const uint32_t e = ws[j] & 0xffu;
+          const float scale = __uint_as_float(e == 0 ? 0x00400000u : e << 23);
+          const uint32_t c = wc[j][q];
+          d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 0));
+          d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 1));
+          d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 2));
+          d[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 3));
+        } else {
+          const uint32_t c0w = wc[j][2 * q], c1w = wc[j][2 * q + 1];
+          d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c0w, 1.0f, false));
+          d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c0w, 1.0f, true));
+          d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c1w, 1.0f, false));
+          d[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c1w, 1.0f, true));
+        }
+        b[j][q] = __builtin_bit_cast(bf16x8, make_uint4(d[0], d[1], d[2], d[3]));
+      }
+    }
+  };
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  const int total = K / 64;
+  const int last = total - 1;
+  dma(0, 0);
+  dma(1, min(1, last));
+  sync();  // step 0 landed
+  dma(2, min(2, last));
+  read(0);
+  __builtin_amdgcn_sched_barrier(0);
+  int cur = 0;
+  for (int t = 0; t < total; ++t) {
+    const int nxt = cur == kStages - 1 ? 0 : cur + 1;
+    convert();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i][0]), b[j][0], acc[i][j],
+                                                            0, 0, 0);
+    sync();
+    dma(cur, min(t + 3, last));
+    const unsigned char *base = lds + nxt * L::kStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[i][0] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c0);
+    read_w(base);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i][1]), b[j][1], acc[i][j],
+                                                            0, 0, 0);
+      fa[i][1] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c1);
+    }
+    // Keep the reads of step t + 1 in this step, ahead of the next
+    // conversion and chunk-0 MFMAs.
+    __builtin_amdgcn_sched_barrier(0);
+    cur = nxt;
+  }
+
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  float *exchange = reinterpret_cast<float *>(lds);
+  if (g == 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) exchange[((p * 8 + i * 2 + j) * 16 + v) * L2C_WAVE + lane] = acc[i][j][v];
+  }
+  __syncthreads();
+  if (g == 0) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = wn * 64 + 32 * j + r;
+      float rscale = 1.0f;
+      if constexpr (!L::kMx) rscale = n < nrows ? static_cast<const float *>(scales)[n0 + n] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int m = wm * 128 + 32 * i + 8 * (v / 4) + 4 * h + v % 4;
+          const float sum = acc[i][j][v] + exchange[((p * 8 + i * 2 + j) * 16 + v) * L2C_WAVE + lane];
+          if (m < mrows && n < nrows) out[static_cast<size_t>(m0 + m) * N + n0 + n] = sum * rscale;
+        }
+    }
+  }
+}
+
+}  // namespace
+
+// Called by l2c_matmul_q after its argument checks, for cols % 64 == 0 (and,
+// for MXFP4, scales at an even address: the scale DMAs read 2 bytes).
+int l2c_matmul_q_ks(float *out, const uint16_t *X, const uint8_t *Wq, const void *scales, int fmt, int batch,
+                    int cols, int rows, hipStream_t stream) {
+  if (cols % 64 != 0 || (fmt != L2C_Q_MXFP4 && fmt != L2C_Q_FP8)) return hipErrorInvalidValue;
+  if (fmt == L2C_Q_MXFP4 && (reinterpret_cast<uintptr_t>(scales) & 1u)) return hipErrorInvalidValue;
+  if (static_cast<long long>(kBM) * cols * 2 > 0x7fffffffLL) return hipErrorInvalidValue;
+  const long long tiles = static_cast<long long>((batch + kBM - 1) / kBM) * ((rows + kBN - 1) / kBN);
+  if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>(tiles)), block(kThreads);
+  if (fmt == L2C_Q_MXFP4)
+    hipLaunchKernelGGL(qgemm_ks_kernel<L2C_Q_MXFP4>, grid, block, 0, stream, out, X, Wq, scales, batch, rows, cols);
+  else
+    hipLaunchKernelGGL(qgemm_ks_kernel<L2C_Q_FP8>, grid, block, 0, stream, out, X, Wq, scales, batch, rows, cols);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+int l2c_qgemm_ks_occupancy(int fmt, int *blocks_per_cu) {
+  const void *fn = fmt == L2C_Q_MXFP4 ? reinterpret_cast<const void *>(qgemm_ks_kernel<L2C_Q_MXFP4>)
+                                      : reinterpret_cast<const void *>(qgemm_ks_kernel<L2C_Q_FP8>);
+  return static_cast<int>(hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, kThreads, 0));
+}
