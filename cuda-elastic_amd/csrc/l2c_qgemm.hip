@@ -296,8 +296,11 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(float *__restrict__ out
       for (int j = 0; j < kFragN; ++j) {
         uint32_t d[4];
         if constexpr (FMT == L2C_Q_MXFP4) {
-          const float scale = __uint_as_float(kok ? f.s[j] : 0u);
-          const uint32_t c = f.w[j][0][q];  // codes k = 8q .. 8q + 7, two per byte
+          // Lanes past K get zero codes, not a zero scale: the scaled
+          // conversion reads only the scale's exponent field, so a scale of
+          // 0.0 multiplies by 2^-127 rather than by zero.
+          const float scale = __uint_as_float(f.s[j]);
+          const uint32_t c = kok ? f.w[j][0][q] : 0u;  // codes k = 8q .. 8q + 7, two per byte
           d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 0));
           d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 1));
           d[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 2));

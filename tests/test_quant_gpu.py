@@ -97,3 +97,51 @@ def test_matmul_q(torch_gpu, l2c, orc, fmt, batch, size, rows):
     assert np.all(np.isfinite(got))
     assert np.max(err / np.maximum(mag, 1e-30)) <= 2e-3
     assert np.all(err <= orc.gamma(size) * mag + np.finfo(np.float32).tiny)
+
+
+def extreme_blocks(rng, rows, size):
+    """Weights whose 32-value blocks span every magnitude class of the MXFP4
+    block scale: zero blocks, blocks below 6 * 2^-126 (scale byte 0, i.e.
+    2^-127, whose bf16 expansions are subnormal), and 1e-20 to 1e30. Rows
+    r % 8 == 7 hold only the smallest class."""
+    W = rng.standard_normal(rows * size).astype(np.float32).reshape(rows, size // 32, 32)
+    mags = np.array([0.0, 3e-38, 1e-20, 1.0, 1e20, 1e30], np.float32)
+    for r in range(rows):
+        for b in range(size // 32):
+            W[r, b] *= mags[1] if r % 8 == 7 else mags[(r + b) % mags.size]
+    return W.reshape(-1)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+@pytest.mark.parametrize("batch,size,rows", [(64, 1024, 96), (40, 96, 72)])
+def test_matmul_q_extreme_blocks(torch_gpu, l2c, orc, fmt, batch, size, rows):
+    """Scale extremes through the contraction (K % 64 == 0 and == 32 kernels)
+    against the exact dequantize-then-accumulate oracle, to the bound of
+    test_matmul_q."""
+    torch = torch_gpu
+    print(f"case matmul_q extremes fmt={fmt} batch={batch} size={size} rows={rows}", flush=True)
+    rng = np.random.default_rng(size + rows)
+    W = extreme_blocks(rng, rows, size)
+    x = rng.standard_normal(batch * size).astype(np.float32)
+    xbf = torch.empty(batch * size, dtype=torch.int16, device="cuda")
+    l2c.to_bf16(xbf, dev(torch, x), batch * size)
+    if fmt == 0:
+        codes = torch.empty(rows * size // 2, dtype=torch.uint8, device="cuda")
+        scales = torch.empty(rows * size // 32, dtype=torch.uint8, device="cuda")
+        l2c.quantize_mxfp4(codes, scales, dev(torch, W), rows, size)
+    else:
+        codes = torch.empty(rows * size, dtype=torch.uint8, device="cuda")
+        scales = torch.empty(rows, dtype=torch.float32, device="cuda")
+        l2c.quantize_fp8(codes, scales, dev(torch, W), rows, size)
+    out = torch.full((batch * rows,), float("nan"), dtype=torch.float32, device="cuda")
+    l2c.matmul_q(out, xbf, codes, scales, fmt, batch, size, rows)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    ref, mag = orc.qmatmul_ref(fmt, xbf.cpu().numpy().view(np.uint16), codes.cpu().numpy(),
+                               scales.cpu().numpy(), size, rows, list(range(batch)), batch)
+    if fmt == 0:
+        assert np.any(scales.cpu().numpy() == 0)  # the 2^-127 scale is exercised
+    err = np.abs(got - ref)
+    assert np.all(np.isfinite(got))
+    bad = err > orc.gamma(size) * mag + np.finfo(np.float32).tiny
+    assert not np.any(bad), (np.argwhere(bad.reshape(batch, rows))[:5], got[bad][:5], ref[bad][:5])
