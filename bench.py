@@ -15,8 +15,8 @@ the graph/direct and copy/nocopy splits are reported under "lines".
 The harness runs in this process (libl2c_host.so via ctypes): HIP events on
 each operation's own stream time the kernels, so `roofline` comes from the
 same run. cpu_baseline times the oracle's fp32 CPU iteration (llama2.c loop
-order) on this host over a bounded sample of the headline shape and scales it
-to one whole iteration.
+order, OpenMP over this host's cores) over a bounded sample of the headline
+shape and scales it to one whole iteration; the double oracle is timed apart.
 
 Usage: python bench.py [--gpus N] [--steps K] [--warmup W] [--quick]
 """
@@ -125,37 +125,62 @@ def lowprec_line(l2c, case, mode="graph", iterations=10, warmup=3):
             "note": "implementation check and accuracy are separate runs (tests/test_lowprec_app_gpu.py)"}
 
 
-def cpu_baseline(batch, size, rows, sample_vectors, sample_rows_norm):
-    """The oracle's fp32 iteration (llama2.c loop order, one thread) on a
-    bounded sample, scaled to one whole iteration of batch x size x rows."""
+def cpu_threads():
+    """The host cores this process may use: its affinity set, capped by
+    OMP_NUM_THREADS when set (the GPU boxes set it to the box's CPU share)."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(cap))) if cap.isdigit() and int(cap) > 0 else n
+
+
+def cpu_baseline(batch, size, rows, sample_vectors, repeats=3):
+    """The oracle's fp32 iteration (llama2.c loop order) on the host's cores
+    (OpenMP over rows and vectors): rmsnorm and softmax of every vector and
+    the product of sample_vectors of them against all rows, each the median
+    of `repeats` runs, the product scaled linearly to the whole batch (every
+    vector costs the same). The double oracle (the validation reference) is
+    timed apart on one thread."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle
 
     L = oracle.lib()
-    inp = oracle.fill("scaled", 1, sample_rows_norm, size, rows)
-    f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
-    n = np.empty(sample_rows_norm * size, np.float32)
-    s = np.empty(sample_rows_norm * size, np.float32)
-    p = np.empty(sample_rows_norm * rows, np.float32)
-    # rmsnorm + softmax over sample_rows_norm vectors, no product.
+    threads = cpu_threads()
+    t_start = time.perf_counter()
+    inp = oracle.fill("scaled", 1, batch, size, rows)
+    n = np.empty(batch * size, np.float32)
+    s = np.empty(batch * size, np.float32)
+    p = np.empty(batch * rows, np.float32)
+
+    def median_time(fn):
+        times = []
+        for _ in range(repeats):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return sorted(times)[len(times) // 2]
+
+    t_vec = median_time(lambda: L.orc_iteration_f32_mt(inp.input, inp.probabilities, inp.weight, inp.matrix,
+                                                         batch, size, 0, 1, 0, n, s, p, threads))
+    t_mm = median_time(lambda: L.orc_iteration_f32_mt(inp.input, inp.probabilities, inp.weight, inp.matrix,
+                                                        0, size, rows, 1, sample_vectors, n, s, p, threads))
+    per_iter_s = t_vec + t_mm * batch / sample_vectors
+    # Double oracle: the product reference and tolerance of 4 vectors.
+    dv = 4
     t0 = time.perf_counter()
-    L.orc_iteration_f32(inp.input, inp.probabilities, inp.weight, inp.matrix, sample_rows_norm, size,
-                        0, 1, 0, n, s, p)
-    t_vec = time.perf_counter() - t0
-    # The product of sample_vectors vectors against all rows (batched order).
-    t0 = time.perf_counter()
-    L.orc_iteration_f32(inp.input, inp.probabilities, inp.weight, inp.matrix, 0, size, rows, 1,
-                        sample_vectors, n, s, p)
-    t_mm = time.perf_counter() - t0
-    per_iter_s = t_vec * batch / sample_rows_norm + t_mm * batch / sample_vectors
+    oracle.product_check(False, True, inp.input, inp.matrix, p, batch, size, rows, list(range(dv)))
+    t_dbl = time.perf_counter() - t0
     return {
-        "value": per_iter_s * 1e6, "unit": "us/iter", "cores": 1, "kind": "port",
-        "sample": (f"oracle orc_iteration_f32 (fp32, llama2.c loop order, 1 thread): rmsnorm+softmax "
-                   f"of {sample_rows_norm} of {batch} vectors ({t_vec:.2f} s) and the product of "
-                   f"{sample_vectors} of {batch} vectors x {rows} rows x {size} ({t_mm:.2f} s), "
-                   f"scaled linearly to one {batch}x{size}x{rows} iteration"),
-        "measured_s": t_vec + t_mm,
+        "value": per_iter_s * 1e6, "unit": "us/iter", "cores": threads, "kind": "port",
+        "sample": (f"oracle orc_iteration_f32_mt (fp32, llama2.c loop order, {threads} OpenMP threads): "
+                   f"rmsnorm+softmax of all {batch} vectors ({t_vec:.3f} s) and the product of "
+                   f"{sample_vectors} of {batch} vectors x {rows} rows x {size} ({t_mm:.2f} s), medians "
+                   f"of {repeats}, the product scaled linearly to one {batch}x{size}x{rows} iteration"),
+        "double_oracle": {
+            "value": t_dbl * batch / dv * 1e6, "unit": "us/iter", "cores": 1,
+            "sample": f"orc_product_check (double reference + tolerance) of {dv} vectors x {rows} rows x "
+                      f"{size} ({t_dbl:.2f} s), scaled to {batch} vectors"},
+        "measured_s": time.perf_counter() - t_start,
     }
 
 
@@ -233,7 +258,7 @@ def main():
     }
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(B, S, R, sample_vectors=192, sample_rows_norm=512)
+        cpu = cpu_baseline(B, S, R, sample_vectors=256)
         log(f"[bench] cpu baseline {cpu['value'] / 1e6:.1f} s/iter ({cpu['measured_s']:.1f} s measured)")
         cpu.pop("measured_s")
     us = headline["gpu_ms_per_iter"] * 1000.0

@@ -20,10 +20,13 @@
  *   orc_mxfp4_exponent            : closed form 6 * 2^X <= amax < 6 * 2^(X+1)
  *   orc_iteration_f32             : llama2.c loop order; pinned against the
  *                                   double references within fp32 bounds
+ *   orc_iteration_f32_mt          : the same loops split over OpenMP threads
+ *                                   (rows and vectors); bit-equal to
+ *                                   orc_iteration_f32 (tests/test_oracle.py)
  *   orc_matvec_fma                : bit-exact sequential fmaf chain; pinned by
  *                                   the deterministic closed form and the
  *                                   double reference
- * Build: oracle/Makefile (gcc, -O2, no fast-math, -ffp-contract=off).
+ * Build: oracle/Makefile (gcc, -O2, -fopenmp, no fast-math, -ffp-contract=off).
  */
 #include <float.h>
 #include <math.h>
@@ -306,6 +309,54 @@ void orc_iteration_f32(const float *input, const float *probabilities, const flo
         product[matmul_batched ? (size_t)b * rows + r : (size_t)r] = val;
       }
     }
+  }
+}
+
+/* orc_iteration_f32 over `threads` OpenMP threads: each normalized or softmax
+ * row and each product output is computed by one thread with the same
+ * sequential loops, so the results equal orc_iteration_f32's bit for bit. */
+void orc_iteration_f32_mt(const float *input, const float *probabilities, const float *weight,
+                          const float *matrix, int batch, int size, int rows, int matmul_batched,
+                          int matmul_vectors, float *normalized, float *softmax, float *product,
+                          int threads) {
+  const int nv = matmul_batched ? matmul_vectors : 1;
+  long long t;
+  if (threads < 1) threads = 1;
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (t = 0; t < 2LL * batch; ++t) {
+    const int b = (int)(t / 2);
+    int j;
+    if (t % 2 == 0) {
+      const float *x = input + (size_t)b * size;
+      float *o = normalized + (size_t)b * size;
+      float ss = 0.0f;
+      for (j = 0; j < size; ++j) ss += x[j] * x[j];
+      ss /= (float)size;
+      ss += 1e-5f;
+      ss = 1.0f / sqrtf(ss);
+      for (j = 0; j < size; ++j) o[j] = weight[j] * (ss * x[j]);
+    } else {
+      const float *pr = probabilities + (size_t)b * size;
+      float *o = softmax + (size_t)b * size;
+      float mx = pr[0], sum = 0.0f;
+      for (j = 1; j < size; ++j)
+        if (pr[j] > mx) mx = pr[j];
+      for (j = 0; j < size; ++j) {
+        o[j] = expf(pr[j] - mx);
+        sum += o[j];
+      }
+      for (j = 0; j < size; ++j) o[j] /= sum;
+    }
+  }
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (t = 0; t < (long long)nv * rows; ++t) {
+    const int b = (int)(t / rows), r = (int)(t % rows);
+    const float *x = input + (size_t)b * size;
+    const float *w = matrix + (size_t)r * size;
+    float val = 0.0f;
+    int j;
+    for (j = 0; j < size; ++j) val += w[j] * x[j];
+    product[matmul_batched ? (size_t)b * rows + r : (size_t)r] = val;
   }
 }
 

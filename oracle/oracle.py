@@ -55,6 +55,7 @@ def lib():
                                     _c.POINTER(d), _c.POINTER(d)]
     L.orc_product_check.restype = i
     L.orc_iteration_f32.argtypes = [_f32p, _f32p, _f32p, _f32p, i, i, i, i, i, _f32p, _f32p, _f32p]
+    L.orc_iteration_f32_mt.argtypes = [_f32p, _f32p, _f32p, _f32p, i, i, i, i, i, _f32p, _f32p, _f32p, i]
     L.orc_matvec_fma.argtypes = [_f32p, _f32p, i, i, _f32p]
     L.orc_e2m1_value.argtypes, L.orc_e2m1_value.restype = [_c.c_uint], d
     L.orc_ue4m3_value.argtypes, L.orc_ue4m3_value.restype = [_c.c_uint], d
@@ -182,6 +183,17 @@ def iteration_f32(inputs: Inputs, batch, size, rows, batched=False, vectors=None
     product = np.empty((batch * rows) if batched else rows, np.float32)
     lib().orc_iteration_f32(inputs.input, inputs.probabilities, inputs.weight, inputs.matrix, batch,
                             size, rows, int(batched), nv, normalized, soft, product)
+    return normalized, soft, product
+
+
+def iteration_f32_mt(inputs: Inputs, batch, size, rows, batched=False, vectors=None, threads=1):
+    """iteration_f32 over OpenMP threads (the timed CPU baseline)."""
+    nv = (vectors if vectors is not None else batch) if batched else 1
+    normalized = np.empty(batch * size, np.float32)
+    soft = np.empty(batch * size, np.float32)
+    product = np.empty((batch * rows) if batched else rows, np.float32)
+    lib().orc_iteration_f32_mt(inputs.input, inputs.probabilities, inputs.weight, inputs.matrix, batch,
+                               size, rows, int(batched), nv, normalized, soft, product, threads)
     return normalized, soft, product
 
 

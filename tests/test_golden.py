@@ -150,3 +150,16 @@ def test_e2m1_roundtrip_and_ties(orc):
     ties = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0])
     np.testing.assert_array_equal(orc.e2m1_encode(ties), [0, 2, 2, 4, 4, 6, 6])
     assert orc.e2m1_encode(np.array([100.0]))[0] == 7
+
+
+@pytest.mark.parametrize("batched", [False, True])
+def test_iteration_f32_threads_bit_equal(orc, batched):
+    """The threaded CPU baseline computes every output with the scalar
+    restatement's loops: equal bit for bit at any thread count."""
+    batch, size, rows = 7, 333, 129
+    inp = orc.fill("scaled", 3, batch, size, rows)
+    ref = orc.iteration_f32(inp, batch, size, rows, batched=batched, vectors=batch)
+    for threads in (1, 3, 8):
+        got = orc.iteration_f32_mt(inp, batch, size, rows, batched=batched, vectors=batch, threads=threads)
+        for a, b in zip(got, ref):
+            np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
