@@ -14,6 +14,14 @@
 // `copy` runs a plain 16-byte-per-lane copy of BATCH x SIZE floats (read
 // once, written once): the calibration kernel for the FETCH_SIZE/WRITE_SIZE
 // counters.
+//
+//   l2c_kernel_bench ceiling
+// measures the matrix-core rate the contractions can reach: register-only
+// loops (no memory traffic) of v_mfma_f32_32x32x2_f32, v_mfma_f32_32x32x16_bf16
+// and the scaled E3M2 v_mfma_scale_f32_32x32x64_f8f6f4, two waves per SIMD,
+// eight independent accumulators, on constant and on random operands. The
+// random-operand rate is the one real data meets (the matrix cores' power
+// draw depends on the operand bits).
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -59,9 +67,124 @@ __global__ void fill_kernel(float *p, size_t n, unsigned seed, float scale) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core ceilings.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ unsigned mix32(unsigned x) {
+  x ^= x >> 15;
+  x *= 2246822519u;
+  x ^= x >> 13;
+  x *= 3266489917u;
+  return x ^ (x >> 16);
+}
+
+enum { kCeilF32 = 0, kCeilBf16 = 1, kCeilFp6 = 2 };
+
+// Each lane holds four operand sets; MFMA (q, t) multiplies set q by set
+// (q + t) % 4 into accumulator t. RANDOM: operand bits from a hash (fp32 and
+// bf16 values with exponents near 1, any 6-bit codes); else a constant.
+template <int TYPE, int RANDOM>
+__global__ __launch_bounds__(512) void ceiling_kernel(float *out, int n) {
+  const unsigned id = blockIdx.x * 512 + threadIdx.x;
+  f32x16 c[8];
+  for (int t = 0; t < 8; ++t)
+    for (int v = 0; v < 16; ++v) c[t][v] = 0.0f;
+  if constexpr (TYPE == kCeilF32) {
+    float a[4], b[4];
+    for (int q = 0; q < 4; ++q) {
+      a[q] = RANDOM ? __uint_as_float((mix32(id * 8 + q) & 0x807fffffu) | 0x3f000000u) : 1.0f;
+      b[q] = RANDOM ? __uint_as_float((mix32(id * 8 + q + 4) & 0x807fffffu) | 0x3f000000u) : 1.0f;
+    }
+    for (int i = 0; i < n; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) c[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q], b[(q + t) & 3], c[t], 0, 0, 0);
+  } else if constexpr (TYPE == kCeilBf16) {
+    u32x4 a[4], b[4];
+    for (int q = 0; q < 4; ++q)
+      for (int v = 0; v < 4; ++v) {
+        a[q][v] = RANDOM ? (mix32(id * 32 + q * 4 + v) & 0x83ff83ffu) | 0x3c003c00u : 0x3c003c00u;
+        b[q][v] = RANDOM ? (mix32(id * 32 + 16 + q * 4 + v) & 0x83ff83ffu) | 0x3c003c00u : 0x3c003c00u;
+      }
+    for (int i = 0; i < n; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          c[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[q]),
+                                                         __builtin_bit_cast(bf16x8, b[(q + t) & 3]), c[t], 0, 0, 0);
+  } else {
+    i32x8 a[4], b[4];
+    for (int q = 0; q < 4; ++q)
+      for (int v = 0; v < 8; ++v) {
+        a[q][v] = v < 6 ? static_cast<int>(RANDOM ? mix32(id * 64 + q * 8 + v) : 0x30c30c30u) : 0;
+        b[q][v] = v < 6 ? static_cast<int>(RANDOM ? mix32(id * 64 + 32 + q * 8 + v) : 0x30c30c30u) : 0;
+      }
+    for (int i = 0; i < n; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          c[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[q], b[(q + t) & 3], c[t], 3, 3, 0, 127, 0, 127);
+  }
+  float sum = 0.0f;
+  for (int t = 0; t < 8; ++t)
+    for (int v = 0; v < 16; ++v) sum += c[t][v];
+  out[id] = sum;
+}
+
+template <int TYPE, int RANDOM>
+static double ceiling_rate(float *out, int blocks, int n) {
+  for (int w = 0; w < 3; ++w) hipLaunchKernelGGL((ceiling_kernel<TYPE, RANDOM>), dim3(blocks), dim3(512), 0, nullptr, out, n);
+  CHECK(hipGetLastError());
+  hipEvent_t a, b;
+  CHECK(hipEventCreate(&a));
+  CHECK(hipEventCreate(&b));
+  const int reps = 5;
+  CHECK(hipEventRecord(a));
+  for (int r = 0; r < reps; ++r)
+    hipLaunchKernelGGL((ceiling_kernel<TYPE, RANDOM>), dim3(blocks), dim3(512), 0, nullptr, out, n);
+  CHECK(hipEventRecord(b));
+  CHECK(hipEventSynchronize(b));
+  float ms = 0.0f;
+  CHECK(hipEventElapsedTime(&ms, a, b));
+  CHECK(hipEventDestroy(a));
+  CHECK(hipEventDestroy(b));
+  const double mnk = TYPE == kCeilF32 ? 32.0 * 32 * 2 : TYPE == kCeilBf16 ? 32.0 * 32 * 16 : 32.0 * 32 * 64;
+  const double flops = 2.0 * mnk * 32.0 * n * reps * blocks * 8.0;  // 32 MFMAs a loop trip, 8 waves a block
+  return flops / (ms * 1e9);
+}
+
+static int run_ceilings() {
+  int cus = 0;
+  CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+  const int blocks = cus;  // one 512-lane block per CU: two waves per SIMD
+  float *out = nullptr;
+  CHECK(hipMalloc(&out, static_cast<size_t>(blocks) * 512 * 4));
+  const char *names[3] = {"fp32 32x32x2", "bf16 32x32x16", "fp6 (E3M2, scaled) 32x32x64"};
+  const int trips[3] = {400, 2000, 2000};
+  for (int type = 0; type < 3; ++type) {
+    double rc = 0, rr = 0;
+    for (int rep = 0; rep < 2; ++rep) {  // the second pass is reported (clocks settled)
+      if (type == 0) rc = ceiling_rate<kCeilF32, 0>(out, blocks, trips[0]), rr = ceiling_rate<kCeilF32, 1>(out, blocks, trips[0]);
+      if (type == 1) rc = ceiling_rate<kCeilBf16, 0>(out, blocks, trips[1]), rr = ceiling_rate<kCeilBf16, 1>(out, blocks, trips[1]);
+      if (type == 2) rc = ceiling_rate<kCeilFp6, 0>(out, blocks, trips[2]), rr = ceiling_rate<kCeilFp6, 1>(out, blocks, trips[2]);
+    }
+    std::printf("ceiling mfma=%s constant_tflops=%.1f random_tflops=%.1f\n", names[type], rc, rr);
+  }
+  CHECK(hipFree(out));
+  return 0;
+}
+
 int main(int argc, char **argv) {
+  if (argc == 2 && std::strcmp(argv[1], "ceiling") == 0) return run_ceilings();
   if (argc != 6) {
-    std::fprintf(stderr, "Usage: %s OP BATCH SIZE ROWS ITERS\n", argv[0]);
+    std::fprintf(stderr, "Usage: %s OP BATCH SIZE ROWS ITERS | %s ceiling\n", argv[0], argv[0]);
     return 2;
   }
   const std::string op = argv[1];
