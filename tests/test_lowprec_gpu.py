@@ -115,8 +115,9 @@ def check_bound(got, A, W, alpha, K):
     assert not bad.any(), f"{bad.sum()} logits outside the bound; first at {np.argwhere(bad)[0]}"
 
 
+# The last two: many tiles ragged on both edges, and the XCD-ordered tile map.
 @pytest.mark.parametrize("batch,cols,rows", [(5, 128, 9), (300, 1024, 260), (1024, 4096, 512), (40, 96, 33),
-                                             (257, 2080, 129)])
+                                             (257, 2080, 129), (1030, 640, 8000), (1024, 1024, 8192)])
 def test_matmul_bf16_bound(torch_gpu, l2c, batch, cols, rows):
     torch = torch_gpu
     print(f"case matmul_bf16 {batch}x{cols}x{rows}", flush=True)
@@ -131,10 +132,15 @@ def test_matmul_bf16_bound(torch_gpu, l2c, batch, cols, rows):
     A = lo.bf16_value(xb).reshape(batch, cols)
     W = lo.bf16_value(wb).reshape(rows, cols)
     check_bound(out.cpu().numpy(), A, W, 0.375, cols)
-    # Without alpha.
+    # Without alpha, twice: equal bit for bit.
     l2c.matmul_bf16(out, dev(torch, xb.view(np.int16)), dev(torch, wb.view(np.int16)), batch, cols, rows)
     torch.cuda.synchronize()
-    check_bound(out.cpu().numpy(), A, W, 1.0, cols)
+    first = out.cpu().numpy().copy()
+    check_bound(first, A, W, 1.0, cols)
+    out.fill_(np.nan)
+    l2c.matmul_bf16(out, dev(torch, xb.view(np.int16)), dev(torch, wb.view(np.int16)), batch, cols, rows)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), first.view(np.uint32))
 
 
 @pytest.mark.parametrize("batch,cols,rows", [(3, 128, 5), (130, 256, 130), (257, 512, 130), (1024, 2048, 1024),
