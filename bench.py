@@ -197,7 +197,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported on this build "
-              "(every GPU box has one MI355X; see DESIGN.md for how the path would shard)",
+              "(every GPU box has one MI355X; the path would shard W and the output rows across GPUs, "
+              "one all-gather of outputs being the only exchange)",
               file=sys.stderr)
         return 2
     import l2c

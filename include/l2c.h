@@ -105,7 +105,9 @@ int l2c_matmul(float *out, const float *X, const float *W, int batch, int cols, 
  * Quantized-weight contraction:
  *   out[b][r] = sum_k Xbf16[b][k] * dequant(Wq, scales)[r][k]
  * Xbf16: batch x cols bfloat16 (uint16 bit patterns); fmt: enum l2c_qformat.
- * L2C_Q_MXFP4 needs cols % 32 == 0; L2C_Q_FP8 any cols.
+ * Both formats need cols % 32 == 0 (l2c_quantize_fp8 itself takes any cols);
+ * Xbf16 and Wq 16-byte aligned. cols % 64 == 0 runs the k-slice kernel
+ * (MXFP4 scales at an even address), other shapes the first design.
  * No counterpart kernel in the reference (see the file header).
  */
 int l2c_matmul_q(float *out, const void *Xbf16, const void *Wq, const void *scales, int fmt,
