@@ -57,6 +57,17 @@ def test_quantized_variants(l2c, variant, inputs):
         assert code == 0 and rec["valid"] == 1 and rec["strict_valid"] == 1, raw
 
 
+@pytest.mark.parametrize("variant,inputs", [("mxfp4", "normal=1"), ("fp8", "normal=2")])
+def test_quantized_sheet_shape(l2c, variant, inputs):
+    """C5 at its configured shape, 1024 x 16384 x 8192 (the k-slice kernel),
+    validated by the harness as the bench runs it."""
+    for mode, copies in (("graph", "nocopy"), ("direct", "copy")):
+        args = [mode, 3, 1024, 16384, 8192, 1, 1, copies, variant, inputs]
+        print("case", " ".join(map(str, args)), flush=True)
+        code, rec, raw = run(l2c, args)
+        assert code == 0 and rec["valid"] == 1 and rec["strict_valid"] == 1, raw
+
+
 def _oracle_recheck(orc, dump, mode_name, seed):
     """Regenerates the inputs and re-validates a dump with the oracle."""
     b, s, r = dump["batch"], dump["size"], dump["rows"]
