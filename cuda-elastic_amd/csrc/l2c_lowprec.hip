@@ -22,8 +22,9 @@
 //    significant bits and lies in [2^-10, 2688], so the bf16 value is exact:
 //    it is the operand form the bf16 matrix cores multiply.
 //
-// Every quantizer reads its input once, coalesced: a group of 8 (MXFP6) or 4
-// (NVFP4) lanes shares one block, each lane holding 4 consecutive floats;
+// Every quantizer reads its input once, coalesced. MXFP6: two lanes a block,
+// 16 consecutive floats each, one workgroup per 3 KB output tile. NVFP4: a
+// group of 4 lanes shares one block, each lane holding 4 consecutive floats;
 // the block maximum is a butterfly over the group.
 #include "l2c_common.h"
 #include "l2c_formats.h"
@@ -39,48 +40,58 @@ __device__ __forceinline__ float group_max(float v, int lanes) {
   return v;
 }
 
-// One group of 8 lanes per 32-value block. Blocks are numbered in output
-// order, id = ((t * Rp / 32 + group) * 4 + b) * 32 + r for row 32 group + r and
-// block 4 t + b of the row, so block id's codes are bytes [24 id, 24 id + 24)
-// and a wave's groups write 192 contiguous bytes; each group reads its block's
-// 128 input bytes at once. Rows past `rows` are padding: zero codes and scale.
+// One workgroup per output tile: k-step t (128 values) of the 32 rows of
+// group g, whose codes are 3 KB contiguous in the tiled layout (block b of row
+// r at byte (b * 32 + r) * 24) and whose scale words are 128 B contiguous.
+// Thread i takes half h = i % 2 of block b = (i / 2) % 4 of row r = i / 8:
+// 16 values, read as 64 contiguous bytes (the 8 threads of a row read its
+// 512 bytes side by side). The block maximum is one shuffle between the two
+// halves; a half's 16 codes are exactly dwords 3h .. 3h + 2 of the block's
+// 24-byte stream (value i at bits 6i .. 6i + 5). Rows past `rows` are
+// padding: zero codes and scale.
 __global__ __launch_bounds__(kThreads) void quantize_mxfp6_kernel(uint8_t *__restrict__ codes,
                                                                   uint8_t *__restrict__ scales,
                                                                   const float *__restrict__ x, int rows,
-                                                                  int width, long long blocks) {
-  const long long gid = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
-  const long long blk = gid / 8;
-  const int j = static_cast<int>(gid % 8);
+                                                                  int width) {
   const int Rp = (rows + 31) / 32 * 32;
-  const int r = static_cast<int>(blk % 32);
-  const int b = static_cast<int>((blk / 32) % 4);
-  const long long tg = blk / 128;  // t * (Rp / 32) + group
-  const int group = static_cast<int>(tg % (Rp / 32));
-  const long long t = tg / (Rp / 32);
-  const int row = group * 32 + r;
-  const bool live = blk < blocks;
-  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if (live && row < rows)
-    v = reinterpret_cast<const float4 *>(x + static_cast<size_t>(row) * width + (4 * t + b) * 32)[j];
-  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  amax = group_max(amax, 8);
+  const int groups = Rp / 32;
+  const int t = static_cast<int>(blockIdx.x) / groups, g = static_cast<int>(blockIdx.x) % groups;
+  const int i = threadIdx.x;
+  const int r = i >> 3, b = (i >> 1) & 3, h = i & 1;
+  const int row = g * 32 + r;
+  float v[16];
+  if (row < rows) {
+    const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<size_t>(row) * width + t * 128 + b * 32 +
+                                                         h * 16);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4 q = src[c];
+      v[4 * c] = q.x, v[4 * c + 1] = q.y, v[4 * c + 2] = q.z, v[4 * c + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = 0.0f;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) amax = fmaxf(amax, fabsf(v[k]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, L2C_WAVE));
   const int X = l2c::mxfp6_exponent(amax);
   const float inv = l2c::pow2_neg(X);
-  unsigned p = 0;
+  unsigned w[3] = {0u, 0u, 0u};
   if (amax > 0.0f) {
-    p = l2c::e3m2_code(v.x * inv) | (l2c::e3m2_code(v.y * inv) << 6) | (l2c::e3m2_code(v.z * inv) << 12) |
-        (l2c::e3m2_code(v.w * inv) << 18);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const unsigned c = l2c::e3m2_code(v[k] * inv);
+      const int pos = 6 * k, word = pos / 32, sh = pos % 32;
+      w[word] |= c << sh;
+      if (sh > 26) w[word + 1] |= c >> (32 - sh);
+    }
   }
-  // Lane j holds bits 24j..24j+23 of the block's 192; lane d < 6 writes dword
-  // d = bits 32d..32d+31, taken from lanes lo = 4d / 3 and lo + 1.
-  const int base = (threadIdx.x % L2C_WAVE) & ~7;
-  const int d = j < 6 ? j : 5;
-  const int lo = (4 * d) / 3, off = 32 * d - 24 * lo;
-  const unsigned plo = static_cast<unsigned>(__shfl(static_cast<int>(p), base + lo, L2C_WAVE));
-  const unsigned phi = static_cast<unsigned>(__shfl(static_cast<int>(p), base + lo + 1, L2C_WAVE));
-  const unsigned word = (plo >> off) | (phi << (24 - off));
-  if (live && j < 6) reinterpret_cast<unsigned *>(codes + blk * 24)[j] = word;
-  if (live && j == 0) scales[(t * Rp + row) * 4 + b] = amax > 0.0f ? static_cast<uint8_t>(X + 127) : 0;
+  const size_t tile = static_cast<size_t>(t) * groups + g;
+  unsigned *dst = reinterpret_cast<unsigned *>(codes + tile * 3072 + (b * 32 + r) * 24 + h * 12);
+  dst[0] = w[0], dst[1] = w[1], dst[2] = w[2];
+  if (h == 0) scales[(static_cast<size_t>(t) * Rp + row) * 4 + b] = amax > 0.0f ? static_cast<uint8_t>(X + 127) : 0;
 }
 
 // Partial maxima of |x| over a grid-stride walk; one per workgroup.
@@ -196,11 +207,10 @@ extern "C" int l2c_quantize_mxfp6(uint8_t *codes, uint8_t *scales, const float *
   if (rows == 0) return hipSuccess;
   if (!codes || !scales || !x || !l2c_aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 3u))
     return hipErrorInvalidValue;
-  const long long blocks = static_cast<long long>((rows + 31) / 32 * 32) * (width / 32);
-  unsigned grid;
-  if (!grid_ok(blocks * 8, &grid)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(quantize_mxfp6_kernel, dim3(grid), dim3(kThreads), 0, stream, codes, scales, x, rows, width,
-                     blocks);
+  const long long tiles = static_cast<long long>((rows + 31) / 32) * (width / 128);
+  if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(quantize_mxfp6_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream, codes,
+                     scales, x, rows, width);
   L2C_LAUNCH_CHECK();
   return hipSuccess;
 }
