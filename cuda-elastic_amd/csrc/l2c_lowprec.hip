@@ -23,9 +23,8 @@
 //    it is the operand form the bf16 matrix cores multiply.
 //
 // Every quantizer reads its input once, coalesced. MXFP6: two lanes a block,
-// 16 consecutive floats each, one workgroup per 3 KB output tile. NVFP4: a
-// group of 4 lanes shares one block, each lane holding 4 consecutive floats;
-// the block maximum is a butterfly over the group.
+// 16 consecutive floats each, one workgroup per 3 KB output tile. NVFP4: one
+// lane a 16-value block.
 #include "l2c_common.h"
 #include "l2c_formats.h"
 #include "../../include/l2c.h"
@@ -34,11 +33,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kAmaxBlocks = 1024;  // partial maxima of the tensor-scale pass
-
-__device__ __forceinline__ float group_max(float v, int lanes) {
-  for (int off = 1; off < lanes; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, L2C_WAVE));
-  return v;
-}
 
 // One workgroup per output tile: k-step t (128 values) of the 32 rows of
 // group g, whose codes are 3 KB contiguous in the tiled layout (block b of row
@@ -133,9 +127,12 @@ __global__ __launch_bounds__(kThreads) void nvfp4_scales_kernel(float *__restric
   }
 }
 
-// One group of 4 lanes per 16-value block: scale code UE4M3((a / 6) s), codes
-// E2M1((v s) / f), each step an FP32 operation in this order; a zero scale
-// code zeroes the block. Optionally also the exact bf16 values code * f.
+// Scale code UE4M3((a / 6) s), codes E2M1((v s) / f), each step an FP32
+// operation in this order; a zero scale code zeroes the block. Optionally also
+// the exact bf16 values code * f. One lane per 16-value block: it reads the
+// block's 64 bytes, takes the block maximum in registers and writes its 8 code
+// bytes (element 2i in the low nibble of byte i), its scale byte and its 32
+// bytes of bf16 expansion; consecutive lanes write consecutive blocks.
 __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(uint8_t *__restrict__ codes,
                                                                   uint8_t *__restrict__ scales,
                                                                   uint16_t *__restrict__ expanded,
@@ -143,32 +140,39 @@ __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(uint8_t *__res
                                                                   const float *__restrict__ tensor_scales,
                                                                   long long blocks) {
 #pragma clang fp contract(off)
-  const long long gid = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
-  const long long blk = gid / 4;
-  const int j = static_cast<int>(gid % 4);
-  const bool live = blk < blocks;
-  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if (live) v = reinterpret_cast<const float4 *>(x)[blk * 4 + j];
-  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  amax = group_max(amax, 4);
+  const long long blk = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+  if (blk >= blocks) return;
+  const float4 *src = reinterpret_cast<const float4 *>(x) + blk * 4;
+  float e[16];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 v = src[q];
+    e[4 * q] = v.x, e[4 * q + 1] = v.y, e[4 * q + 2] = v.z, e[4 * q + 3] = v.w;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(e[i]));
   const float s = tensor_scales[0];
   const unsigned sc = l2c::nvfp4_scale_code(amax, s);
   const float f = l2c::ue4m3_value(sc);
-  const float e[4] = {v.x, v.y, v.z, v.w};
-  unsigned c[4] = {0, 0, 0, 0};
-  if (sc != 0) {
+  unsigned c[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) c[i] = l2c::nvfp4_code(e[i], s, f);
+  for (int i = 0; i < 16; ++i) c[i] = sc != 0 ? l2c::nvfp4_code(e[i], s, f) : 0u;
+  unsigned lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    lo |= c[i] << (4 * i);
+    hi |= c[8 + i] << (4 * i);
   }
-  if (!live) return;
-  reinterpret_cast<uint16_t *>(codes)[blk * 4 + j] =
-      static_cast<uint16_t>(c[0] | (c[1] << 4) | (c[2] << 8) | (c[3] << 12));
-  if (j == 0) scales[blk] = static_cast<uint8_t>(sc);
+  reinterpret_cast<uint2 *>(codes)[blk] = make_uint2(lo, hi);
+  scales[blk] = static_cast<uint8_t>(sc);
   if (expanded) {
-    unsigned b[4];
+    unsigned b[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) b[i] = __float_as_uint(l2c::e2m1_value(c[i]) * f) >> 16;  // exact
-    reinterpret_cast<uint2 *>(expanded)[blk * 4 + j] = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+    for (int i = 0; i < 16; ++i) b[i] = __float_as_uint(l2c::e2m1_value(c[i]) * f) >> 16;  // exact
+    uint4 *dst = reinterpret_cast<uint4 *>(expanded) + blk * 2;
+    dst[0] = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
+    dst[1] = make_uint4(b[8] | (b[9] << 16), b[10] | (b[11] << 16), b[12] | (b[13] << 16), b[14] | (b[15] << 16));
   }
 }
 
@@ -234,12 +238,12 @@ extern "C" int l2c_quantize_nvfp4(uint8_t *codes, uint8_t *scales, uint16_t *exp
                                   const float *tensor_scales, int rows, int width, hipStream_t stream) {
   if (rows < 0 || width <= 0 || width % 16 != 0) return hipErrorInvalidValue;
   if (rows == 0) return hipSuccess;
-  if (!codes || !scales || !x || !tensor_scales || !l2c_aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 1u) ||
-      (expanded_bf16 && (reinterpret_cast<uintptr_t>(expanded_bf16) & 7u)))
+  if (!codes || !scales || !x || !tensor_scales || !l2c_aligned16(x) || (reinterpret_cast<uintptr_t>(codes) & 7u) ||
+      (expanded_bf16 && !l2c_aligned16(expanded_bf16)))
     return hipErrorInvalidValue;
   const long long blocks = static_cast<long long>(rows) * (width / 16);
   unsigned grid;
-  if (!grid_ok(blocks * 4, &grid)) return hipErrorInvalidValue;
+  if (!grid_ok(blocks, &grid)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(quantize_nvfp4_kernel, dim3(grid), dim3(kThreads), 0, stream, codes, scales, expanded_bf16,
                      x, tensor_scales, blocks);
   L2C_LAUNCH_CHECK();

@@ -157,6 +157,7 @@ int l2c_to_bf16(uint16_t *out, const float *in, size_t n, hipStream_t stream);
  *   value, FP32 operations in this order; a zero scale code zeroes the block.
  *   s is read from tensor_scales[0] on the device. expanded_bf16 (optional,
  *   [rows][width]) receives each element's exact value code * f as bf16.
+ *   x and expanded_bf16 16-byte aligned, codes 8-byte aligned.
  * l2c_to_bf16_x4: l2c_to_bf16 for n % 4 == 0 and 16-byte aligned input.
  */
 #define L2C_NVFP4_PARTIALS 1024
