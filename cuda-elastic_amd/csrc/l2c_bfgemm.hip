@@ -20,8 +20,15 @@
 //    side, so 16 lanes reading one chunk of 16 consecutive rows hit 16 distinct
 //    slots of the 64 banks. Each of a lane's six instructions has its own
 //    clamped per-lane source offset; the step's k offset is scalar.
-//  * Three stages: step t's DMA is issued at step t - 2 and waited (vmcnt)
-//    before the barrier of step t - 1.
+//  * Three stages, one barrier a step: the chunk-0 MFMAs of step t, the
+//    barrier (the DMA of step t + 1 landed, every wave's reads of step t
+//    done), the DMA of step t + 3 into the stage step t occupied, then the
+//    chunk-1 MFMAs with the reads of step t + 1 between them. A step's DMA
+//    has two steps to land.
+//  * Bounds, measured at 1024 x 16384 x 8192: the L2-to-LDS staging of this
+//    tiling (about 17 TB/s; the compulsory misses, all of X read by each XCD,
+//    set it) and the bf16 matrix cores' rate on random operands (about 1.8
+//    PFLOP/s, a power limit).
 //  * Every access is in bounds by construction (no reliance on buffer range
 //    checks): lanes whose row is past the tile's rows load the last row instead
 //    (those rows are never stored). K % 64 == 0; l2c_matmul_bf16 routes
