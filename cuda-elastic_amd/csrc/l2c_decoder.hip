@@ -178,6 +178,95 @@ __global__ __launch_bounds__(kThreads) void decoder_rmsnorm_regs_kernel(float *n
   }
 }
 
+// The VEC register-resident rmsnorm over ROWS consecutive sequences per
+// workgroup, software-pipelined: row r + 1's loads are issued before row r is
+// reduced and stored, so reads and writes overlap inside a CU instead of the
+// whole grid reading, then writing. The norm weight is loaded once. Per row the
+// arithmetic, and its order, are those of decoder_rmsnorm_regs_kernel.
+template <int CHUNKS>
+__device__ __forceinline__ void rms_row_load(float4 (&dst)[CHUNKS], const float *embedding, int token, int vocab,
+                                             int width, int t) {
+  const bool ok = token >= 0 && token < vocab;
+  const float4 *x4 = reinterpret_cast<const float4 *>(embedding + static_cast<size_t>(ok ? token : 0) * width);
+  const int n4 = width / 4;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c)
+    dst[c] = ok && t + c * kThreads < n4 ? x4[t + c * kThreads] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
+template <int CHUNKS>
+__device__ __forceinline__ void rms_row_store(float *o, const float4 (&v)[CHUNKS], const float4 (&g)[CHUNKS],
+                                              bool ok, float *slots, int width, int t) {
+#pragma clang fp contract(off)
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    ss += v[c].x * v[c].x;
+    ss += v[c].y * v[c].y;
+    ss += v[c].z * v[c].z;
+    ss += v[c].w * v[c].w;
+  }
+  ss = group_sum(ss, slots);
+  ss /= static_cast<float>(width);
+  ss += 1e-5f;
+  const float scale = 1.0f / sqrtf(ss);
+  float4 *o4 = reinterpret_cast<float4 *>(o);
+  const int n4 = width / 4;
+  const float nan = __builtin_nanf("");
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int i = t + c * kThreads;
+    if (i < n4)
+      o4[i] = ok ? make_float4(g[c].x * (scale * v[c].x), g[c].y * (scale * v[c].y), g[c].z * (scale * v[c].z),
+                               g[c].w * (scale * v[c].w))
+                 : make_float4(nan, nan, nan, nan);
+  }
+}
+
+// Two rows a workgroup (221 VGPRs, two workgroups a CU) against one row a
+// workgroup at 1024 x 16384, same box: 24.5 against 26.4 µs in the decoder,
+// 24.0 / 28.2 / 26.7 against 26.3 / 29.3 / 27.8 µs in the lowprec fp32 / bf16 /
+// NVFP4 steps, 27.9 against 26.9 µs in the MXFP6 step; four rows (one
+// workgroup a CU) measured 28.7 µs. Used from this batch up, where the grid
+// still gives every CU two workgroups.
+constexpr int kRowsPipelineMinBatch = 512;
+
+template <int CHUNKS, int ROWS>
+__global__ __launch_bounds__(kThreads) void decoder_rmsnorm_rows_kernel(float *normalized, const int *tokens,
+                                                                        const float *embedding,
+                                                                        const float *weight, int width,
+                                                                        int vocab, int batch) {
+  static_assert(ROWS % 2 == 0, "rows alternate between two register sets");
+  __shared__ float slots[2][kWaves];
+  const int t = threadIdx.x;
+  const int first = blockIdx.x * ROWS;
+  float4 g[CHUNKS], a[CHUNKS], b[CHUNKS];
+  const float4 *w4 = reinterpret_cast<const float4 *>(weight);
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c)
+    g[c] = t + c * kThreads < width / 4 ? w4[t + c * kThreads] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  int token_a = tokens[first];  // first < batch: the grid is ceil(batch / ROWS)
+  rms_row_load(a, embedding, token_a, vocab, width, t);
+#pragma unroll
+  for (int r = 0; r < ROWS; r += 2) {
+    // Row first + r is in a; first + r + 1 goes to b.
+    const bool has_b = first + r + 1 < batch;
+    const int token_b = has_b ? tokens[first + r + 1] : -1;
+    if (has_b) rms_row_load(b, embedding, token_b, vocab, width, t);
+    rms_row_store(normalized + static_cast<size_t>(first + r) * width, a, g, token_a >= 0 && token_a < vocab,
+                  slots[0], width, t);
+    if (!has_b) break;  // uniform across the workgroup
+    const bool has_a = r + 2 < ROWS && first + r + 2 < batch;
+    if (has_a) {
+      token_a = tokens[first + r + 2];
+      rms_row_load(a, embedding, token_a, vocab, width, t);
+    }
+    rms_row_store(normalized + static_cast<size_t>(first + r + 1) * width, b, g, token_b >= 0 && token_b < vocab,
+                  slots[1], width, t);
+    if (!has_a) break;
+  }
+}
+
 // (value, index) maximum over the workgroup with ties to the smaller index;
 // the result is valid in lane 0. INT_MAX marks "no candidate".
 __device__ __forceinline__ int group_argmax(float best, int best_index, float *vslots, int *islots) {
@@ -404,7 +493,11 @@ extern "C" int l2c_decoder_rmsnorm(float *normalized, const int *tokens, const f
   if (!normalized || !tokens || !embedding || !weight) return hipErrorInvalidValue;
   const bool vec = width % 4 == 0 && l2c_aligned16(normalized) && l2c_aligned16(embedding) &&
                    l2c_aligned16(weight);
-  if (const RmsFn regs = vec ? rmsnorm_regs<true>(width) : rmsnorm_regs<false>(width)) {
+  const int per_lane = (width + kThreads - 1) / kThreads;
+  if (vec && per_lane > 32 && per_lane <= 64 && batch >= kRowsPipelineMinBatch) {
+    hipLaunchKernelGGL((decoder_rmsnorm_rows_kernel<16, 2>), dim3((batch + 1) / 2), dim3(kThreads), 0, stream,
+                       normalized, tokens, embedding, weight, width, vocab, batch);
+  } else if (const RmsFn regs = vec ? rmsnorm_regs<true>(width) : rmsnorm_regs<false>(width)) {
     hipLaunchKernelGGL(regs, dim3(batch), dim3(kThreads), 0, stream, normalized, tokens, embedding, weight, width,
                        vocab);
   } else if (vec)

@@ -29,7 +29,9 @@ def test_init_model_exact(torch_gpu, l2c, width, vocab):
     np.testing.assert_array_equal(w.cpu().numpy(), g)
 
 
-@pytest.mark.parametrize("width,vocab,batch", [(96, 16, 40), (4100, 300, 9), (1001, 77, 30), (2, 2, 3)])
+@pytest.mark.parametrize("width,vocab,batch", [(96, 16, 40), (4100, 300, 9), (1001, 77, 30), (2, 2, 3),
+                                               (16384, 40, 7), (16384, 40, 513), (12000, 33, 520),
+                                               (16384, 64, 1024)])
 def test_rmsnorm_synthetic_exact(torch_gpu, l2c, width, vocab, batch):
     """The contract's float32 order on the synthetic model, bit for bit; an
     invalid token gives a NaN row."""
@@ -50,10 +52,11 @@ def test_rmsnorm_synthetic_exact(torch_gpu, l2c, width, vocab, batch):
             assert np.isnan(got[b]).all()
 
 
-def test_rmsnorm_general_rows(torch_gpu, l2c):
+@pytest.mark.parametrize("width,vocab,batch", [(3000, 50, 64), (16384, 50, 65), (16384, 50, 601)])
+def test_rmsnorm_general_rows(torch_gpu, l2c, width, vocab, batch):
     """Arbitrary embedding rows: within 2e-6 relative of the double result."""
     torch = torch_gpu
-    width, vocab, batch = 3000, 50, 64
+    print(f"case decoder_rmsnorm general width={width} batch={batch}", flush=True)
     rng = np.random.default_rng(11)
     e = rng.standard_normal((vocab, width)).astype(np.float32)
     w = rng.uniform(0.5, 1.5, width).astype(np.float32)
@@ -66,13 +69,14 @@ def test_rmsnorm_general_rows(torch_gpu, l2c):
     assert dorc.within(out.cpu().numpy().reshape(batch, width), ref, 2e-6).all()
 
 
-@pytest.mark.parametrize("vocab,batch", [(8192, 33), (1000, 17), (77, 5), (2, 4)])
+@pytest.mark.parametrize("vocab,batch", [(8192, 33), (1000, 17), (77, 5), (2, 4), (8192, 513), (6000, 520)])
 def test_softmax_argmax(torch_gpu, l2c, vocab, batch):
     torch = torch_gpu
     print(f"case decoder_softmax_argmax vocab={vocab} batch={batch}", flush=True)
     rng = np.random.default_rng(vocab)
     logits = (rng.standard_normal((batch, vocab)) * 3).astype(np.float32)
     logits[0, :] = 0.5  # all equal: the first maximum is index 0
+    logits[batch - 2, :] = 0.25  # again in a later row (the second of a two-row workgroup)
     steps, step = 3, 1
     probs = torch.empty(batch * vocab, dtype=torch.float32, device="cuda")
     tokens = torch.full((batch,), -5, dtype=torch.int32, device="cuda")
@@ -86,23 +90,28 @@ def test_softmax_argmax(torch_gpu, l2c, vocab, batch):
     assert dorc.within(p, ref, dorc.PROBABILITY_RELATIVE).all()
     want = np.argmax(p, axis=1)  # first maximum of the float32 probabilities
     assert np.array_equal(tokens.cpu().numpy(), want)
-    assert want[0] == 0
+    assert want[0] == 0 and want[batch - 2] == 0
     g = generated.cpu().numpy().reshape(batch, steps)
     assert np.array_equal(g[:, step], want)
     assert (g[:, 0] == -7).all() and (g[:, 2] == -7).all()
 
 
-def test_softmax_argmax_nan_row(torch_gpu, l2c):
+@pytest.mark.parametrize("vocab,batch,nan_rows", [(64, 2, [1]), (8192, 600, [1, 300, 599])])
+def test_softmax_argmax_nan_row(torch_gpu, l2c, vocab, batch, nan_rows):
+    """A row of NaN logits has no maximum: token -1 (first and second row of a
+    two-row workgroup alike)."""
     torch = torch_gpu
-    vocab, batch = 64, 2
+    print(f"case decoder_softmax_argmax nan rows vocab={vocab} batch={batch}", flush=True)
     logits = np.zeros((batch, vocab), np.float32)
-    logits[1] = np.nan
+    logits[nan_rows] = np.nan
     probs = torch.empty(batch * vocab, dtype=torch.float32, device="cuda")
     tokens = torch.zeros(batch, dtype=torch.int32, device="cuda")
     generated = torch.zeros(batch * 2, dtype=torch.int32, device="cuda")
     l2c.decoder_softmax_argmax(probs, dev(torch, logits), tokens, generated, vocab, batch, 2, 0)
     torch.cuda.synchronize()
-    assert tokens.cpu().numpy().tolist() == [0, -1]
+    want = np.zeros(batch, np.int32)
+    want[nan_rows] = -1
+    assert tokens.cpu().numpy().tolist() == want.tolist()
 
 
 @pytest.mark.parametrize("batch,width,vocab,steps", [(40, 96, 16, 5), (70, 200, 33, 4), (3, 2, 2, 2),
