@@ -5,7 +5,7 @@
 // of its operands with alpha = d_X * d_W (experiments/blackwell/lowprec/
 // spec.json "cases"; the reference runs CUTLASS GEMMs, decoder_lowprec.cu:82-121).
 //
-// Kernel design (the structure of the MXFP6 contraction in l2c_mxgemm.hip):
+// Kernel design:
 //  * v_mfma_f32_32x32x16_bf16. Tile 256 (batch) x 128 (rows) x 64 (k per step),
 //    8 wavefronts: waves w and w + 4 share a SIMD and the same 128 x 64 output
 //    sub-tile (4 x 2 blocks of 32 x 32); wave group g = w / 4 takes the step's
@@ -20,15 +20,20 @@
 //    side, so 16 lanes reading one chunk of 16 consecutive rows hit 16 distinct
 //    slots of the 64 banks. Each of a lane's six instructions has its own
 //    clamped per-lane source offset; the step's k offset is scalar.
-//  * Three stages, one barrier a step: the chunk-0 MFMAs of step t, the
-//    barrier (the DMA of step t + 1 landed, every wave's reads of step t
-//    done), the DMA of step t + 3 into the stage step t occupied, then the
-//    chunk-1 MFMAs with the reads of step t + 1 between them. A step's DMA
-//    has two steps to land.
-//  * Bounds, measured at 1024 x 16384 x 8192: the L2-to-LDS staging of this
-//    tiling (about 17 TB/s; the compulsory misses, all of X read by each XCD,
-//    set it) and the bf16 matrix cores' rate on random operands (about 1.8
-//    PFLOP/s, a power limit).
+//  * Ping-pong schedule (as in l2c_qgemm_ks.hip): the two waves of a SIMD
+//    run half a step apart. A wave's memory phase of step t issues the DMA of
+//    step t + 2 into the stage step t - 1 held, reads its fragments of step t
+//    and waits for its DMA of step t + 1; its MFMA phase runs the step's 16
+//    MFMAs at raised wave priority. Group 0 (waves 0-3) and group 1 (waves
+//    4-7) alternate the phases with a workgroup barrier after each, so each
+//    SIMD's matrix core takes one wave's MFMAs while the other wave reads LDS.
+//    Three stages (144 KB); a step's DMA has one step to land.
+//  * Bounds, measured at 1024 x 16384 x 8192: the ping-pong form 227 against
+//    239 µs for the earlier schedule (both waves of a SIMD in step, one
+//    barrier a step; the matrix cores busy 58% of the time) on the same box;
+//    waiting for the DMA a phase later, or no wave priority, measured the
+//    same. Each memory phase moves about 72 KB through LDS (48 KB of fragment
+//    reads, 24 KB of DMA), against 512 MFMA cycles.
 //  * Every access is in bounds by construction (no reliance on buffer range
 //    checks): lanes whose row is past the tile's rows load the last row instead
 //    (those rows are never stored). K % 64 == 0; l2c_matmul_bf16 routes
@@ -99,9 +104,16 @@ __global__ __launch_bounds__(kThreads, 1) void bf16_gemm_kernel(float *__restric
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + kXBytes + (8 * k + wave) * 1024), 16, wsrc[k],
                                                128 * t, 0, 0);
   };
-  auto sync = [&]() __attribute__((always_inline)) {
+  // This wave's DMA of the step before the newest has landed (six
+  // instructions a step), its LDS reads are done; then the workgroup barrier.
+  auto wait_dma_barrier = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto barrier = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
   // Fragments: rows wm * 128 + 32 i + r (X) and wn * 64 + 32 j + r (W); chunk
@@ -110,7 +122,6 @@ __global__ __launch_bounds__(kThreads, 1) void bf16_gemm_kernel(float *__restric
   const int a0 = (wm * 128 + r) * 128, b0 = kXBytes + (wn * 64 + r) * 128;
   const int c0 = 16 * ((4 * h + 2 * g) ^ sw), c1 = 16 * ((4 * h + 2 * g + 1) ^ sw);
   u32x4 fa[4][2], fb[2][2];
-  // Chunk 0's six reads, then chunk 1's, in the order the main loop uses.
   auto read = [&](int stage) __attribute__((always_inline)) {
     const unsigned char *base = lds + stage * kStage;
 #pragma unroll
@@ -129,65 +140,38 @@ __global__ __launch_bounds__(kThreads, 1) void bf16_gemm_kernel(float *__restric
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-  // MFMAs of the wave's k-chunk q (8 per step).
-  auto mma = [&](int q) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i][q]),
-                                                            __builtin_bit_cast(bf16x8, fb[j][q]), acc[i][j], 0, 0, 0);
-  };
 
-  // Step t: chunk-0 MFMAs of F(t); barrier (DMA(t + 1) landed, every wave's
-  // reads of F(t) from stage t % 3 done); DMA(t + 3) into stage t % 3; chunk-1
-  // MFMAs of F(t) interleaved with the reads of F(t + 1): chunk 0's registers
-  // are free at once, each chunk-1 register right after its last MFMA. LDS and
-  // the matrix cores then work at the same time; DMA keeps two steps to land.
   const int total = K / 64;
   const int last = total - 1;
   dma(0, 0);
   dma(1, min(1, last));
-  sync();  // step 0 landed
-  dma(2, min(2, last));
-  read(0);
-  __builtin_amdgcn_sched_barrier(0);
+  wait_dma_barrier();  // step 0 landed everywhere
+  if (g == 1) barrier();
   int cur = 0;
   for (int t = 0; t < total; ++t) {
-    const int nxt = cur == kStages - 1 ? 0 : cur + 1;
-    mma(0);
-    sync();
-    dma(cur, min(t + 3, last));
-    const unsigned char *base = lds + nxt * kStage;
+    // Memory phase of step t: DMA of step t + 2 into the stage step t - 1
+    // held, the fragment reads of step t, a wait for this wave's DMA of step
+    // t + 1.
+    const int free_stage = cur == 0 ? kStages - 1 : cur - 1;
+    dma(free_stage, min(t + 2, last));
+    read(cur);
+    wait_dma_barrier();
+    // MFMA phase of step t.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i][0] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c0);
+    for (int q = 0; q < 2; ++q)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) fb[j][0] = *reinterpret_cast<const u32x4 *>(base + b0 + 4096 * j + c0);
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i][1]),
-                                                            __builtin_bit_cast(bf16x8, fb[j][1]), acc[i][j], 0, 0, 0);
-      fa[i][1] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c1);
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) fb[j][1] = *reinterpret_cast<const u32x4 *>(base + b0 + 4096 * j + c1);
-    // Order of the region after the barrier: the six DMA instructions and the
-    // six chunk-0 reads first, then MFMA pairs each followed by one read.
-    __builtin_amdgcn_sched_group_barrier(0x020, 6, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    // Keep the reads of F(t + 1) in this step: the next step's chunk-0 MFMAs
-    // must find them already in flight.
-    __builtin_amdgcn_sched_barrier(0);
-    cur = nxt;
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i][q]),
+                                                              __builtin_bit_cast(bf16x8, fb[j][q]), acc[i][j], 0, 0,
+                                                              0);
+    __builtin_amdgcn_s_setprio(0);
+    barrier();
+    cur = cur == kStages - 1 ? 0 : cur + 1;
   }
+  if (g == 0) barrier();
 
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   float *exchange = reinterpret_cast<float *>(lds);

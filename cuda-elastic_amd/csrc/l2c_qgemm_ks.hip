@@ -4,37 +4,47 @@
 // l2c_quantize_fp8 write (codes row-major, MXFP4 scales [rows][K/32]).
 // l2c_matmul_q routes K % 64 == 32 to the kernel in l2c_qgemm.hip.
 //
-// Kernel design (the structure of the bf16 contraction in l2c_bfgemm.hip):
+// Kernel design:
 //  * The product runs on the bf16 matrix cores (v_mfma_f32_32x32x16_bf16);
 //    the weight codes are converted exactly to bf16 in registers by the
 //    gfx950 scaled conversions (v_cvt_scalef32_pk_bf16_fp4 / _fp8), an E2M1
 //    value times 2^(s - 127) or an E4M3 value having at most 4 significant
-//    bits. The fp8 row scale multiplies each output in the epilogue.
+//    bits. The conversion reads only the exponent field of its fp32 scale, so
+//    the E8M0 byte shifted into that field is the scale for every byte value
+//    (byte 0, 0.0f, scales by 2^-127). The fp8 row scale multiplies each
+//    output in the epilogue.
 //  * Tile 256 (batch) x 128 (rows) x 64 (k per step), 8 wavefronts in k-slice
 //    pairs: waves w and w + 4 share a SIMD and a 128 x 64 output sub-tile and
 //    take the step's k-chunks 2g, 2g + 1 (g = w / 4); lane (r, h) of MFMA q
 //    supplies k = 32h + 8q + 0..7 for both operands, so a lane's codes for its
 //    two chunks are 8 contiguous bytes (MXFP4, one scale block h) or 16 (fp8).
 //    The pairs' partial sums are added once at the end through LDS.
+//  * Ping-pong schedule: the two waves of a SIMD run half a step apart. Group
+//    0 (waves 0-3) runs its memory phase of step t -- the DMA of step t + 3
+//    into the stage step t - 1 held, the fragment reads and conversions of
+//    step t, a wait for its DMA of step t + 1 -- while group 1 (waves 4-7)
+//    runs its 16 MFMAs of step t - 1 at raised wave priority; then the roles
+//    swap. A workgroup barrier ends each phase, so each SIMD's matrix core
+//    takes one wave's MFMAs while the other wave waits on LDS and memory.
+//    Group 1 takes one extra barrier at the start and group 0 one at the end,
+//    so every wave passes the same number of barriers.
 //  * LDS DMA staging (buffer_load ... lds): X 32 KB a step as 32 1-KB
 //    instructions (4 a wave); W codes 4 KB (MXFP4, waves 0-3) or 8 KB (fp8,
 //    one a wave); MXFP4 scales as 2-byte DMAs, one row a lane (waves 4, 5),
 //    each landing zero-extended in its own LDS word (a 2-byte DMA writes
-//    lane i's bytes at word i). The weight bytes a step are a quarter (MXFP4)
-//    or half (fp8) of the bf16 weights'.
-//  * Bounds, measured at 1024 x 16384 x 8192: the L2-to-LDS staging rate of
-//    this tiling (about 17 TB/s with the X re-reads across XCDs) and the bf16
-//    matrix cores' rate on random operands (about 1.7 PFLOP/s, against 2.4
-//    on constant data: a power limit). The MXFP4 conversions run on the VALU
-//    beside the other wave's MFMAs.
+//    lane i's bytes at word i). Four stages (146 KB MXFP4, 160 KB fp8): a
+//    stage is free once both groups have read it, and a step's DMA has three
+//    steps to land.
 //  * 16-byte chunks of LDS rows are XOR-swizzled by row bits (X: bits 1..3;
 //    W: bit 3 for 32-byte MXFP4 rows, bits 2..3 for 64-byte fp8 rows), applied
 //    on the DMA's source side, so the fragment reads avoid bank conflicts
 //    (MXFP4's 8-byte reads keep a two-way conflict on 2 KB a wave and step).
-//  * Three stages, one barrier a step: the chunk-0 MFMAs of step t, the
-//    barrier (DMA of step t + 1 landed, every wave's reads of step t done),
-//    the DMA of step t + 3 into the freed stage, then the chunk-1 MFMAs
-//    interleaved with the reads of step t + 1.
+//  * Measured at 1024 x 16384 x 8192 against the earlier schedule (both
+//    waves of a SIMD in step, one barrier a step; the matrix cores busy 55% of
+//    the time): MXFP4 214 against 226-229 µs, fp8 206 against 223-228 µs.
+//    Timing probes with work removed: without the DMA 164 / 175 µs, without
+//    the DMA and the fragment reads 149 / 162 µs (the MFMAs alone on these
+//    operands); removing the conversions or the DMA wait changes nothing.
 //  * Every access is in bounds by construction: rows past the operand are
 //    clamped per lane to its last row; those rows are never stored.
 #include "l2c_common.h"
@@ -51,7 +61,7 @@ typedef __attribute__((address_space(3))) void lds_ptr;
 constexpr int kBM = 256;
 constexpr int kBN = 128;
 constexpr int kThreads = 512;
-constexpr int kStages = 3;
+constexpr int kStages = 4;
 constexpr int kXcds = 8;
 constexpr int kXBytes = kBM * 128;    // 256 rows x 64 bf16
 constexpr int kExchange = 131072;     // 4 sub-tiles x 8 blocks x 16 values x 64 lanes x 4 B
@@ -88,9 +98,9 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
   const int g = wave >> 2, p = wave & 3;
   const int wm = p & 1, wn = p >> 1;
   const int r = lane % 32, h = lane / 32;
-  const int xrb = 2 * K;                  // X bytes per row
-  const int wrb = L::kMx ? K / 2 : K;     // code bytes per W row
-  const int srb = K / 32;                 // MXFP4 scale bytes per row
+  const int xrb = 2 * K;
+  const int wrb = L::kMx ? K / 2 : K;
+  const int srb = K / 32;
   const __amdgpu_buffer_rsrc_t rx =
       l2c::buffer_rsrc(X + static_cast<size_t>(m0) * K, static_cast<uint32_t>(mrows) * xrb);
   const __amdgpu_buffer_rsrc_t rw =
@@ -99,11 +109,6 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
       L::kMx ? l2c::buffer_rsrc(static_cast<const uint8_t *>(scales) + static_cast<size_t>(n0) * srb,
                                 static_cast<uint32_t>(nrows) * srb)
              : rw;
-
-  // DMA sources (per-lane parts; the step's k offset is scalar). X: block b of
-  // 8 rows (b = 8k + wave), lane i fills row 8b + i / 8, slot i % 8 with chunk
-  // (i % 8) ^ xswizzle(row). W: wave w fills rows (64 / lanes-per-row) w + i /
-  // lanes-per-row, slot i % lanes-per-row. Scales: wave 4 + s fills row 64 s + i.
   const int lrow = 8 * wave + lane / 8;
   const int lchunk = 16 * ((lane % 8) ^ xswizzle(lrow));
   int xsrc[4];
@@ -113,6 +118,11 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
   const int wsrc = min(wrow, nrows - 1) * wrb + 16 * ((lane % L::kLanesPerRow) ^ L::wswizzle(wrow));
   const int ssrc = min(max(64 * (wave - 4) + lane, 0), nrows - 1) * srb;
 
+  // DMA sources (per-lane parts; the step's k offset is scalar). X: block b of
+  // 8 rows (b = 8k + wave), lane i fills row 8b + i / 8, slot i % 8 with chunk
+  // (i % 8) ^ xswizzle(row). W: wave w fills rows (64 / lanes-per-row) w + i /
+  // lanes-per-row, slot i % lanes-per-row. Scales: wave 4 + s fills row 64 s +
+  // i. DMA instructions a wave issues a step: 5, or 4 (MXFP4 waves 6 and 7).
   auto dma = [&](int stage, int t) __attribute__((always_inline)) {
     unsigned char *base = lds + stage * L::kStage;
     if constexpr (L::kMx) {
@@ -130,22 +140,26 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr *)(base + (8 * k + wave) * 1024), 16, xsrc[k], 128 * t,
                                                0, 0);
   };
-  // Waits for this wave's DMA of the older of two outstanding steps and its
-  // LDS reads, then the workgroup barrier. DMA instructions a step: 5 (fp8;
-  // MXFP4 waves 0..5), 4 (MXFP4 waves 6, 7).
-  auto sync = [&]() __attribute__((always_inline)) {
+  // This wave's DMA two steps back has landed, its LDS reads are done; then
+  // the workgroup barrier. At most 8 DMA instructions stay in flight: the two
+  // newer steps' for a wave that issues 4 a step, those and 2 more for one
+  // that issues 5 (a stricter wait, and one form for every wave: no branch
+  // for the compiler to sink the conversions past).
+  auto wait_dma_barrier = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
-    if (!L::kMx || wave < 6)
-      asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto barrier = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
 
   // Fragments. X rows wm * 128 + 32 i + r, chunks 4h + 2g (+1). W rows
   // wn * 64 + 32 j + r (the swizzle of row + 32 equals that of row): MXFP4
   // bytes 16h + 8g of the 32-byte row (chunk h), fp8 bytes 32h + 16g (chunk
-  // 2h + g); MXFP4 scale word of the row, byte h.
+  // 2h + g); the MXFP4 scale word of the row (byte h is the lane's block).
   const int xsw = xswizzle(r);
   const int a0 = (wm * 128 + r) * 128;
   const int c0 = 16 * ((4 * h + 2 * g) ^ xsw), c1 = 16 * ((4 * h + 2 * g + 1) ^ xsw);
@@ -154,31 +168,26 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
                         : kXBytes + wr0 * 64 + 16 * ((2 * h + g) ^ L::wswizzle(wr0));
   const int sb = L::kSOff + 4 * wr0;
   u32x4 fa[4][2];
-  u32x4 wc[2];  // MXFP4 uses the low two words
+  u32x4 wc[2];
   uint32_t ws[2];
-  // Codes (and the MXFP4 scale byte h, in the low byte of ws) of a stage.
-  auto read_w = [&](const unsigned char *base) __attribute__((always_inline)) {
+  auto read = [&](int stage) __attribute__((always_inline)) {
+    const unsigned char *base = lds + stage * L::kStage;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       if constexpr (L::kMx) {
         const u32x2 v = *reinterpret_cast<const u32x2 *>(base + wb + 1024 * j);
         wc[j][0] = v[0], wc[j][1] = v[1];
-        ws[j] = *reinterpret_cast<const uint32_t *>(base + sb + 128 * j) >> (8 * h);
+        ws[j] = *reinterpret_cast<const uint32_t *>(base + sb + 128 * j);
       } else {
         wc[j] = *reinterpret_cast<const u32x4 *>(base + wb + 2048 * j);
       }
     }
-  };
-  auto read = [&](int stage) __attribute__((always_inline)) {
-    const unsigned char *base = lds + stage * L::kStage;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i][0] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c0);
-    read_w(base);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i][1] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c1);
+    for (int i = 0; i < 4; ++i) {
+      fa[i][0] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c0);
+      fa[i][1] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c1);
+    }
   };
-  // B operands of the wave's two chunks from the codes: 8 k a chunk, two per
-  // conversion.
   bf16x8 b[2][2];
   auto convert = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -187,9 +196,10 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
       for (int q = 0; q < 2; ++q) {
         uint32_t d[4];
         if constexpr (L::kMx) {
-          // Block scale 2^(e - 127) as fp32 (e = 0 is the subnormal 2^-127).
-          const uint32_t e = ws[j] & 0xffu;
-          const float scale = __uint_as_float(e == 0 ? 0x00400000u : e << 23);
+          // The block's scale byte h as an fp32 exponent field: the
+          // conversion reads only that field, so scale byte 0 (0.0f) scales
+          // by 2^-127, its E8M0 value.
+          const float scale = __uint_as_float(((ws[j] >> (8 * h)) & 0xffu) << 23);
           const uint32_t c = wc[j][q];
           d[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 0));
           d[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 1));
@@ -218,39 +228,29 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
   const int last = total - 1;
   dma(0, 0);
   dma(1, min(1, last));
-  sync();  // step 0 landed
   dma(2, min(2, last));
-  read(0);
-  __builtin_amdgcn_sched_barrier(0);
-  int cur = 0;
+  wait_dma_barrier();  // step 0 landed everywhere
+  if (g == 1) barrier();
   for (int t = 0; t < total; ++t) {
-    const int nxt = cur == kStages - 1 ? 0 : cur + 1;
+    // Memory phase of step t.
+    dma((t + 3) & (kStages - 1), min(t + 3, last));
+    read(t & (kStages - 1));
     convert();
+    wait_dma_barrier();
+    // MFMA phase of step t.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i][0]), b[j][0], acc[i][j],
-                                                            0, 0, 0);
-    sync();
-    dma(cur, min(t + 3, last));
-    const unsigned char *base = lds + nxt * L::kStage;
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i][0] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c0);
-    read_w(base);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i][1]), b[j][1], acc[i][j],
-                                                            0, 0, 0);
-      fa[i][1] = *reinterpret_cast<const u32x4 *>(base + a0 + 4096 * i + c1);
-    }
-    // Keep the reads of step t + 1 in this step, ahead of the next
-    // conversion and chunk-0 MFMAs.
-    __builtin_amdgcn_sched_barrier(0);
-    cur = nxt;
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[i][c]), b[j][c],
+                                                              acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_s_setprio(0);
+    barrier();
   }
+  if (g == 0) barrier();
 
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   float *exchange = reinterpret_cast<float *>(lds);
