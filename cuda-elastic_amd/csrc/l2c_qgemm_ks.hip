@@ -45,6 +45,11 @@
 //    Timing probes with work removed: without the DMA 164 / 175 µs, without
 //    the DMA and the fragment reads 149 / 162 µs (the MFMAs alone on these
 //    operands); removing the conversions or the DMA wait changes nothing.
+//    Three stages for fp8 (128 KB, one step for the DMA) measured 213 µs.
+//    In the C5 iteration (rmsnorm and softmax on two more streams beside
+//    the product) MXFP4 runs 245 against 262 µs; fp8 277 against 262 µs:
+//    its product gets faster (225 against 260 µs on the harness's normal
+//    weights) but the row kernels no longer hide under it.
 //  * Every access is in bounds by construction: rows past the operand are
 //    clamped per lane to its last row; those rows are never stored.
 #include "l2c_common.h"
@@ -61,13 +66,13 @@ typedef __attribute__((address_space(3))) void lds_ptr;
 constexpr int kBM = 256;
 constexpr int kBN = 128;
 constexpr int kThreads = 512;
-constexpr int kStages = 4;
 constexpr int kXcds = 8;
 constexpr int kXBytes = kBM * 128;    // 256 rows x 64 bf16
 constexpr int kExchange = 131072;     // 4 sub-tiles x 8 blocks x 16 values x 64 lanes x 4 B
 
-template <int FMT>
+template <int FMT, int STAGES>
 struct Layout {
+  static constexpr int kStages = STAGES;
   static constexpr bool kMx = FMT == L2C_Q_MXFP4;
   static constexpr int kWRow = kMx ? 32 : 64;  // code bytes per W row and step
   static constexpr int kLanesPerRow = kWRow / 16;
@@ -79,13 +84,13 @@ struct Layout {
 
 __device__ __forceinline__ int xswizzle(int row) { return (row >> 1) & 7; }
 
-template <int FMT>
+template <int FMT, int STAGES>
 __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict__ out,
                                                                const uint16_t *__restrict__ X,
                                                                const uint8_t *__restrict__ Wq,
                                                                const void *__restrict__ scales, int M, int N,
                                                                int K) {
-  using L = Layout<FMT>;
+  using L = Layout<FMT, STAGES>;
   __shared__ __attribute__((aligned(1024))) unsigned char lds[L::kLds];
   int tile = blockIdx.x;
   const int tiles = gridDim.x;
@@ -140,14 +145,18 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr *)(base + (8 * k + wave) * 1024), 16, xsrc[k], 128 * t,
                                                0, 0);
   };
-  // This wave's DMA two steps back has landed, its LDS reads are done; then
-  // the workgroup barrier. At most 8 DMA instructions stay in flight: the two
-  // newer steps' for a wave that issues 4 a step, those and 2 more for one
-  // that issues 5 (a stricter wait, and one form for every wave: no branch
-  // for the compiler to sink the conversions past).
+  // This wave's DMA of the step after the one just read has landed, its LDS
+  // reads are done; then the workgroup barrier. The DMA of the STAGES - 2
+  // newer steps may stay in flight: at most 4 (STAGES - 2) instructions, which
+  // is exact for a wave that issues 4 a step and stricter for one that issues
+  // 5 (one form for every wave: no branch for the compiler to sink the
+  // conversions past).
   auto wait_dma_barrier = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if constexpr (STAGES == 4)
+      asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
   auto barrier = [&]() __attribute__((always_inline)) {
@@ -226,15 +235,16 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
 
   const int total = K / 64;
   const int last = total - 1;
-  dma(0, 0);
-  dma(1, min(1, last));
-  dma(2, min(2, last));
+#pragma unroll
+  for (int st = 0; st < STAGES - 1; ++st) dma(st, min(st, last));
   wait_dma_barrier();  // step 0 landed everywhere
   if (g == 1) barrier();
+  int cur = 0;
   for (int t = 0; t < total; ++t) {
-    // Memory phase of step t.
-    dma((t + 3) & (kStages - 1), min(t + 3, last));
-    read(t & (kStages - 1));
+    // Memory phase of step t: the DMA of step t + STAGES - 1 goes into the
+    // stage step t - 1 held.
+    dma(cur == 0 ? STAGES - 1 : cur - 1, min(t + STAGES - 1, last));
+    read(cur);
     convert();
     wait_dma_barrier();
     // MFMA phase of step t.
@@ -249,6 +259,7 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
                                                               acc[i][j], 0, 0, 0);
     __builtin_amdgcn_s_setprio(0);
     barrier();
+    cur = cur == STAGES - 1 ? 0 : cur + 1;
   }
   if (g == 0) barrier();
 
@@ -293,16 +304,19 @@ int l2c_matmul_q_ks(float *out, const uint16_t *X, const uint8_t *Wq, const void
   const long long tiles = static_cast<long long>((batch + kBM - 1) / kBM) * ((rows + kBN - 1) / kBN);
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(tiles)), block(kThreads);
+  // Four stages for both formats (146 KB MXFP4, 160 KB fp8).
   if (fmt == L2C_Q_MXFP4)
-    hipLaunchKernelGGL(qgemm_ks_kernel<L2C_Q_MXFP4>, grid, block, 0, stream, out, X, Wq, scales, batch, rows, cols);
+    hipLaunchKernelGGL((qgemm_ks_kernel<L2C_Q_MXFP4, 4>), grid, block, 0, stream, out, X, Wq, scales, batch, rows,
+                       cols);
   else
-    hipLaunchKernelGGL(qgemm_ks_kernel<L2C_Q_FP8>, grid, block, 0, stream, out, X, Wq, scales, batch, rows, cols);
+    hipLaunchKernelGGL((qgemm_ks_kernel<L2C_Q_FP8, 4>), grid, block, 0, stream, out, X, Wq, scales, batch, rows,
+                       cols);
   L2C_LAUNCH_CHECK();
   return hipSuccess;
 }
 
 int l2c_qgemm_ks_occupancy(int fmt, int *blocks_per_cu) {
-  const void *fn = fmt == L2C_Q_MXFP4 ? reinterpret_cast<const void *>(qgemm_ks_kernel<L2C_Q_MXFP4>)
-                                      : reinterpret_cast<const void *>(qgemm_ks_kernel<L2C_Q_FP8>);
+  const void *fn = fmt == L2C_Q_MXFP4 ? reinterpret_cast<const void *>(qgemm_ks_kernel<L2C_Q_MXFP4, 4>)
+                                      : reinterpret_cast<const void *>(qgemm_ks_kernel<L2C_Q_FP8, 4>);
   return static_cast<int>(hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, kThreads, 0));
 }
