@@ -116,8 +116,11 @@ def check_bound(got, A, W, alpha, K):
 
 
 # The last two: many tiles ragged on both edges, and the XCD-ordered tile map.
+# (7, 64, 11) and (9, 192, 17): one step and as many steps as the DMA ring has
+# stages (the prologue's clamped DMAs).
 @pytest.mark.parametrize("batch,cols,rows", [(5, 128, 9), (300, 1024, 260), (1024, 4096, 512), (40, 96, 33),
-                                             (257, 2080, 129), (1030, 640, 8000), (1024, 1024, 8192)])
+                                             (257, 2080, 129), (1030, 640, 8000), (1024, 1024, 8192),
+                                             (7, 64, 11), (9, 192, 17)])
 def test_matmul_bf16_bound(torch_gpu, l2c, batch, cols, rows):
     torch = torch_gpu
     print(f"case matmul_bf16 {batch}x{cols}x{rows}", flush=True)

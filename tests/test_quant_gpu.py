@@ -66,11 +66,13 @@ def test_quantize_fp8_exact(torch_gpu, l2c, orc, rows, cols):
 
 
 @pytest.mark.parametrize("fmt", [0, 1])
-# K % 64 == 0 runs l2c_qgemm_ks.hip (the last two: many tiles, ragged edges
-# and the XCD-ordered tile map); K % 64 == 32 runs l2c_qgemm.hip.
+# K % 64 == 0 runs l2c_qgemm_ks.hip ((520, 1088, 1030), (1024, 2048, 1024):
+# many tiles, ragged edges and the XCD-ordered tile map; K = 64, 192, 256: one
+# step, three, and as many steps as the DMA ring has stages); K % 64 == 32
+# runs l2c_qgemm.hip.
 @pytest.mark.parametrize("batch,size,rows", [(8, 64, 16), (300, 1024, 200), (256, 4096, 256),
                                              (33, 96, 77), (5, 32, 9), (130, 2080, 140),
-                                             (520, 1088, 1030), (1024, 2048, 1024)])
+                                             (520, 1088, 1030), (1024, 2048, 1024), (3, 192, 5), (9, 256, 17)])
 def test_matmul_q(torch_gpu, l2c, orc, fmt, batch, size, rows):
     torch = torch_gpu
     print(f"case matmul_q fmt={fmt} batch={batch} size={size} rows={rows}", flush=True)
