@@ -18,9 +18,14 @@
 //    one-pass structure with scalar loads; rows longer than 1024 lanes x 64
 //    floats take a two-pass path that re-reads the row.
 //  * The coalesced matrix-vector product gives each output row to one
-//    wavefront: 64 lanes x 16 B = 1 KiB contiguous per load instruction, W
-//    streamed with nontemporal loads so it does not evict x from L2, several
-//    independent loads in flight per lane, one wave reduction per row.
+//    wavefront: 64 lanes x 16 B = 1 KiB contiguous per load instruction,
+//    several independent loads in flight per lane, one wave reduction per row.
+//    W is read with nontemporal loads (they keep it from evicting x from L2),
+//    except when it is 128-256 MiB: then ordinary loads let the 256 MB MALL
+//    keep it between launches. Measured at 4096 columns, nontemporal against
+//    ordinary loads: 64 MiB 10.1 / 10.8 µs, 96 MiB 15.0 / 15.4, 144 MiB
+//    24.0 / 22.3, 172 MiB 27.2 / 25.7, 256 MiB 39.2 / 37.2, 288 MiB
+//    43.9 / 44.4, 384 MiB 58.0 / 65.1.
 //  * The naive product keeps the reference's one-lane-per-row structure and
 //    its sequential column order (one fused multiply-add per column), so its
 //    result is bit-reproducible by a CPU fmaf chain.
@@ -131,7 +136,7 @@ __global__ __launch_bounds__(256) void matvec_naive_kernel(float *out, const flo
 // One wavefront per output row; kWavesPerBlock rows per block.
 constexpr int kMatvecWaves = 4;
 
-template <bool VEC>
+template <bool VEC, bool NT>
 __global__ __launch_bounds__(kMatvecWaves * L2C_WAVE) void matvec_wave_kernel(
     float *out, const float *x, const float *W, int cols, int rows) {
   const int lane = threadIdx.x % L2C_WAVE;
@@ -146,10 +151,10 @@ __global__ __launch_bounds__(kMatvecWaves * L2C_WAVE) void matvec_wave_kernel(
     int c = lane;
     // Four independent 1 KiB wave loads in flight per step.
     for (; c + 3 * L2C_WAVE < cols4; c += 4 * L2C_WAVE) {
-      const float4 m0 = l2c::ld4_stream(w4 + c);
-      const float4 m1 = l2c::ld4_stream(w4 + c + L2C_WAVE);
-      const float4 m2 = l2c::ld4_stream(w4 + c + 2 * L2C_WAVE);
-      const float4 m3 = l2c::ld4_stream(w4 + c + 3 * L2C_WAVE);
+      const float4 m0 = NT ? l2c::ld4_stream(w4 + c) : w4[c];
+      const float4 m1 = NT ? l2c::ld4_stream(w4 + c + L2C_WAVE) : w4[c + L2C_WAVE];
+      const float4 m2 = NT ? l2c::ld4_stream(w4 + c + 2 * L2C_WAVE) : w4[c + 2 * L2C_WAVE];
+      const float4 m3 = NT ? l2c::ld4_stream(w4 + c + 3 * L2C_WAVE) : w4[c + 3 * L2C_WAVE];
       const float4 v0 = x4[c], v1 = x4[c + L2C_WAVE];
       const float4 v2 = x4[c + 2 * L2C_WAVE], v3 = x4[c + 3 * L2C_WAVE];
       a0 = fmaf(m0.x, v0.x, a0); a0 = fmaf(m0.y, v0.y, a0);
@@ -319,10 +324,14 @@ extern "C" int l2c_matvec(float *out, const float *x, const float *W, int cols, 
   } else {
     const bool vec = cols % 4 == 0 && l2c_aligned16(x) && l2c_aligned16(W);
     const dim3 grid((rows + kMatvecWaves - 1) / kMatvecWaves), block(kMatvecWaves * L2C_WAVE);
-    if (vec)
-      hipLaunchKernelGGL(matvec_wave_kernel<true>, grid, block, 0, stream, out, x, W, cols, rows);
+    const unsigned long long w_bytes = 4ULL * static_cast<unsigned long long>(rows) * cols;
+    const bool mall = w_bytes > (128ULL << 20) && w_bytes <= (256ULL << 20);
+    if (vec && mall)
+      hipLaunchKernelGGL((matvec_wave_kernel<true, false>), grid, block, 0, stream, out, x, W, cols, rows);
+    else if (vec)
+      hipLaunchKernelGGL((matvec_wave_kernel<true, true>), grid, block, 0, stream, out, x, W, cols, rows);
     else
-      hipLaunchKernelGGL(matvec_wave_kernel<false>, grid, block, 0, stream, out, x, W, cols,
+      hipLaunchKernelGGL((matvec_wave_kernel<false, true>), grid, block, 0, stream, out, x, W, cols,
                          rows);
   }
   L2C_LAUNCH_CHECK();
@@ -380,8 +389,8 @@ extern "C" int l2c_launch_shape(int op, int batch, int cols, int rows, int varia
         *grid = (rows + 63) / 64;
         *block = 64;
       } else if (variant == L2C_MATVEC_COALESCED) {
-        fn = cols % 4 == 0 ? reinterpret_cast<const void *>(matvec_wave_kernel<true>)
-                           : reinterpret_cast<const void *>(matvec_wave_kernel<false>);
+        fn = cols % 4 == 0 ? reinterpret_cast<const void *>(matvec_wave_kernel<true, true>)
+                           : reinterpret_cast<const void *>(matvec_wave_kernel<false, true>);
         *grid = (rows + kMatvecWaves - 1) / kMatvecWaves;
         *block = kMatvecWaves * L2C_WAVE;
       } else {
