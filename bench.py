@@ -223,6 +223,8 @@ def main():
             ("c4_fused_graph_nocopy", cfg("graph", 200, B, S, R, "nocopy", "fused")),
             ("c2_gemv_graph_nocopy", cfg("graph", 1000, 1, 4096, 11008, "nocopy", "coalesced", warm=50)),
             ("c2_gemv_direct_nocopy", cfg("direct", 1000, 1, 4096, 11008, "nocopy", "coalesced", warm=50)),
+            ("c2_fused_graph_nocopy", cfg("graph", 1000, 1, 4096, 11008, "nocopy", "fused", warm=50)),
+            ("c2_fused_direct_nocopy", cfg("direct", 1000, 1, 4096, 11008, "nocopy", "fused", warm=50)),
             ("c3_graph_nocopy", cfg("graph", 10000, 8, 768, 2048, "nocopy", "coalesced", warm=100)),
             ("c3_direct_nocopy", cfg("direct", 10000, 8, 768, 2048, "nocopy", "coalesced", warm=100)),
             ("c3_graph_copy", cfg("graph", 10000, 8, 768, 2048, "copy", "coalesced", warm=100)),
