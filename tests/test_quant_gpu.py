@@ -99,6 +99,11 @@ def test_matmul_q(torch_gpu, l2c, orc, fmt, batch, size, rows):
     assert np.all(np.isfinite(got))
     assert np.max(err / np.maximum(mag, 1e-30)) <= 2e-3
     assert np.all(err <= orc.gamma(size) * mag + np.finfo(np.float32).tiny)
+    # A second call into a fresh buffer: equal bit for bit (fixed reduction order).
+    again = torch.full((batch * rows,), float("nan"), dtype=torch.float32, device="cuda")
+    l2c.matmul_q(again, xbf, codes, scales, fmt, batch, size, rows)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(again.cpu().numpy().view(np.uint32), out.cpu().numpy().view(np.uint32))
 
 
 def extreme_blocks(rng, rows, size):
