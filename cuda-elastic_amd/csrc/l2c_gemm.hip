@@ -64,8 +64,10 @@ constexpr int kLoadsA = kBM * kChunksPerRow / kThreads;  // 4
 constexpr int kLoadsB = kBN * kChunksPerRow / kThreads;  // 2
 constexpr int kGroups = kBK / 8;                         // 8-deep k groups per step
 constexpr int kXcds = 8;
-// The tile of one workgroup must stay addressable with 32-bit buffer offsets.
-constexpr long long kMaxTileBytes = 0xffffffffLL;
+// The tile of one workgroup must stay addressable with the kernel's per-lane
+// byte offsets, row * K * 4 computed in (signed) int; larger K takes the
+// generic kernel, which indexes with size_t.
+constexpr long long kMaxTileBytes = 0x7fffffffLL;
 
 static_assert(kBM * kChunksPerRow % kThreads == 0, "A slab must split evenly");
 static_assert(kBN * kChunksPerRow % kThreads == 0, "B slab must split evenly");
@@ -371,7 +373,8 @@ int l2c_gemm_launch_shape(int batch, int cols, int rows, int *grid, int *block,
 
 extern "C" int l2c_matmul(float *out, const float *X, const float *W, int batch, int cols,
                           int rows, hipStream_t stream) {
-  if (batch < 0 || cols <= 0 || rows < 0) return hipErrorInvalidValue;
+  // The generic kernel's k indexes (k + 3 of a 32-wide step) stay below INT_MAX.
+  if (batch < 0 || cols <= 0 || cols > 0x7fffffff - kBK || rows < 0) return hipErrorInvalidValue;
   if (batch == 0 || rows == 0) return hipSuccess;
   if (!out || !X || !W) return hipErrorInvalidValue;
   const long long tiles =

@@ -237,11 +237,13 @@ extern "C" int l2c_matmul_mxfp6(float *out, const uint8_t *X, const uint8_t *Xsc
   if (!out || !X || !Xscales || !W || !Wscales || !l2c_aligned16(X) || !l2c_aligned16(W) ||
       !l2c_aligned16(Xscales) || !l2c_aligned16(Wscales))
     return hipErrorInvalidValue;
-  // Whole operands stay addressable with 32-bit buffer offsets.
+  // Whole operands stay addressable with the kernel's byte offsets, which it
+  // computes in (signed) int.
   size_t xc, xs, wc, ws;
   l2c_mxfp6_bytes(batch, cols, &xc, &xs);
   l2c_mxfp6_bytes(rows, cols, &wc, &ws);
-  if (xc > 0xffffffffULL || wc > 0xffffffffULL) return hipErrorInvalidValue;
+  if (xc > 0x7fffffffULL || wc > 0x7fffffffULL || xs > 0x7fffffffULL || ws > 0x7fffffffULL)
+    return hipErrorInvalidValue;
   const long long tiles = static_cast<long long>((batch + kBM - 1) / kBM) * ((rows + kBN - 1) / kBN);
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
   hipLaunchKernelGGL(mxfp6_gemm_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream, out, X,

@@ -69,8 +69,9 @@ constexpr int kStages = 3;
 constexpr int kXStride = 144;                           // LDS bytes per X row (64 bf16 + 16 pad)
 constexpr int kXChunks = kBM * (kBK / 8) / kThreads;    // 16-byte X chunks per thread and step: 4
 constexpr int kXcds = 8;
-// The X tile of one workgroup must stay addressable with 32-bit offsets.
-constexpr long long kMaxTileBytes = 0xffffffffLL;
+// The X tile of one workgroup must stay addressable with the per-lane byte
+// offsets, row * K * 2 computed in (signed) int.
+constexpr long long kMaxTileBytes = 0x7fffffffLL;
 
 // Per-format staging geometry. W rows hold the step's codes (32 bytes of
 // MXFP4 or 64 of fp8) with 16-byte chunks XOR-swizzled by row bits; MXFP4

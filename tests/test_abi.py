@@ -89,3 +89,43 @@ def test_compare_tool_on_reference_dump(tmp_path, orc):
     code, out = l2c.compare_dumps([src, str(d)])
     assert code == 1 and "header" in out
     assert l2c.compare_dumps([src])[0] == 2
+
+
+def test_k_bound_rejects_offset_overflow():
+    """Contractions whose per-lane byte offsets (row * K * element bytes, in
+    int) would pass INT_MAX are refused before anything is launched, so the
+    calls return on a machine without a GPU."""
+    import l2c
+    lib = ctypes.CDLL(l2c.LIB_PATH)
+    p = ctypes.c_void_p(1 << 20)  # never dereferenced: the call returns first
+    for fn in (lib.l2c_matmul_q, lib.l2c_matmul, lib.l2c_matmul_bf16):
+        fn.restype = ctypes.c_int
+    big = 1 << 22  # 256 rows x 2^22 bf16 = 2^31 bytes
+    for fmt in (0, 1):
+        assert lib.l2c_matmul_q(p, p, p, p, fmt, 1, big, 1, None) == 1
+        assert lib.l2c_matmul_q(p, p, p, p, fmt, 1, big + 32, 1, None) == 1
+    assert lib.l2c_matmul_bf16(p, p, p, None, 1, big, 1, None) == 1
+    assert lib.l2c_matmul_bf16(p, p, p, None, 1, big + 32, 1, None) == 1
+    assert lib.l2c_matmul(p, p, p, 1, 0x7fffffff - 31, 1, None) == 1
+
+
+def test_make_fails_on_compile_error(tmp_path):
+    """A HIP source that does not compile makes the package build exit
+    non-zero and leaves no object behind (no stale object can reach a link)."""
+    import shutil
+    pkg = tmp_path / "pkg"
+    (pkg / "csrc").mkdir(parents=True)
+    (tmp_path / "include").mkdir()
+    (tmp_path / "include" / "l2c.h").write_text("/* empty */\n")
+    shutil.copy(os.path.join(PKG, "Makefile"), pkg / "Makefile")
+    (pkg / "csrc" / "broken.hip").write_text("this is not C++;\n")
+    proc = subprocess.run(["make", "-C", str(pkg), "_build/broken.o"], capture_output=True, text=True,
+                          timeout=300)
+    assert proc.returncode != 0
+    assert not (pkg / "_build" / "broken.o").exists()
+    (pkg / "csrc" / "broken.hip").write_text(
+        "#include <hip/hip_runtime.h>\n__global__ void ok_kernel(int *p) { *p = 1; }\n")
+    proc = subprocess.run(["make", "-C", str(pkg), "_build/broken.o"], capture_output=True, text=True,
+                          timeout=300)
+    assert proc.returncode == 0, proc.stderr
+    assert (pkg / "_build" / "broken.o").exists()

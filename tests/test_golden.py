@@ -163,3 +163,213 @@ def test_iteration_f32_threads_bit_equal(orc, batched):
         got = orc.iteration_f32_mt(inp, batch, size, rows, batched=batched, vectors=batch, threads=threads)
         for a, b in zip(got, ref):
             np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# The quantized-weight recipe (MXFP4 blocks, per-row fp8, the dequantize-then-
+# accumulate reference). The reference has no such kernel; its element rules
+# are experiments/blackwell/lowprec/reference.cpp:13-96 and the block recipe is
+# the benchmark configuration's (X = floor(log2(amax / 6)), e8m0 byte X + 127;
+# per-row fp8 scale amax / 448). These tests build operands whose quantized
+# form is known exactly, from the formats' bit-field definitions (not from the
+# oracle's tables), so a wrong scale offset, block boundary, nibble order,
+# divide-for-multiply or index fails them.
+
+def _e2m1_value(code):
+    """OCP MX E2M1: sign bit 3, exponent bits 2..1 (bias 1), mantissa bit 0."""
+    code = int(code)
+    e, m = (code >> 1) & 3, code & 1
+    mag = m * 0.5 if e == 0 else (1 + m / 2) * 2.0 ** (e - 1)
+    return -mag if code & 8 else mag
+
+
+def _e4m3_value(code):
+    """OCP E4M3FN: sign bit 7, exponent bits 6..3 (bias 7), mantissa bits 2..0."""
+    code = int(code)
+    e, m = (code >> 3) & 15, code & 7
+    mag = m / 8 * 2.0 ** -6 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7)
+    return -mag if code & 0x80 else mag
+
+
+E2M1_VAL = np.array([_e2m1_value(c) for c in range(16)])
+E4M3_VAL = np.array([_e4m3_value(c) if c & 0x7f != 0x7f else np.nan for c in range(256)])
+
+
+def test_format_values_from_bit_fields(orc):
+    """The oracle's value tables equal the bit-field definitions at every code."""
+    for c in range(16):
+        assert orc.lib().orc_e2m1_value(c) == E2M1_VAL[c]
+    for c in range(127):
+        assert orc.lib().orc_ue4m3_value(c) == E4M3_VAL[c]
+    assert E2M1_VAL[7] == 6.0 and E4M3_VAL[0x7e] == 448.0 and E4M3_VAL[1] == 2.0 ** -9
+
+
+def _exact_mxfp4_rows(rng, rows, blocks, exps):
+    """Rows of e2m1 values times 2^X per 32-value block, each block's largest
+    magnitude exactly 6 * 2^X (placed at index 0, 31 or at random)."""
+    codes = rng.integers(0, 16, (rows, blocks, 32))
+    X = rng.choice(exps, (rows, blocks))
+    pos = rng.integers(0, 32, (rows, blocks))
+    pos[:, 0], pos[:, -1] = 0, 31
+    for r in range(rows):
+        for b in range(blocks):
+            codes[r, b, pos[r, b]] = 7 | (8 * rng.integers(0, 2))
+    w = (E2M1_VAL[codes] * np.exp2(X)[:, :, None].astype(np.float64)).astype(np.float32)
+    return codes, X, w.reshape(rows, blocks * 32)
+
+
+def test_mxfp4_row_exact_blocks_roundtrip(orc):
+    """Blocks of e2m1 values times 2^X with amax = 6 * 2^X quantize to exactly
+    those codes (-0 as +0) with scale byte X + 127, and dequantize back to the
+    same floats bit for bit. X covers the clamp (-127) and large exponents."""
+    rng = np.random.default_rng(41)
+    rows, blocks = 6, 24
+    exps = np.concatenate([[-127, -126, -1, 0, 1, 120, 125], rng.integers(-120, 120, 9)])
+    codes, X, w = _exact_mxfp4_rows(rng, rows, blocks, exps)
+    got_codes, got_scales = orc.quantize_mxfp4(w, rows, blocks * 32)
+    np.testing.assert_array_equal(got_scales.reshape(rows, blocks), X + 127)
+    np.testing.assert_array_equal(got_codes.reshape(rows, blocks, 32), np.where(codes == 8, 0, codes))
+    deq = E2M1_VAL[got_codes.reshape(rows, blocks, 32)] * np.exp2(got_scales.reshape(rows, blocks).astype(np.float64) - 127)[:, :, None]
+    np.testing.assert_array_equal(deq.astype(np.float32).reshape(rows, -1), w)
+
+
+def test_mxfp4_row_saturates_and_rounds_to_nearest(orc):
+    """A block maximum in (6, 12) * 2^X keeps X (= floor(log2(amax / 6))) and
+    saturates to 6 * 2^X; every element lands on its nearest e2m1 value times
+    2^X, so the error is at most half that value's spacing."""
+    rng = np.random.default_rng(42)
+    rows, blocks = 5, 20
+    X = rng.integers(-60, 60, (rows, blocks))
+    t = rng.uniform(1.0 + 1e-6, 2.0 - 1e-6, (rows, blocks))
+    amax = (6.0 * t * np.exp2(X)).astype(np.float32)
+    # Edges, in float32: the next float above 6 * 2^X and the last below 12 * 2^X.
+    amax[0, 0] = np.nextafter(np.float32(6.0 * 2.0 ** X[0, 0]), np.float32(np.inf))
+    amax[0, 1] = np.nextafter(np.float32(12.0 * 2.0 ** X[0, 1]), np.float32(0))
+    amax = amax.astype(np.float64)
+    w = rng.uniform(-1.0, 1.0, (rows, blocks, 32)) * amax[:, :, None]
+    pos = rng.integers(0, 32, (rows, blocks))
+    sign = rng.choice([-1.0, 1.0], (rows, blocks))
+    for r in range(rows):
+        for b in range(blocks):
+            w[r, b, pos[r, b]] = sign[r, b] * amax[r, b]
+    w = w.astype(np.float32)
+    codes, scales = orc.quantize_mxfp4(w.reshape(rows, -1), rows, blocks * 32)
+    codes = codes.reshape(rows, blocks, 32)
+    np.testing.assert_array_equal(scales.reshape(rows, blocks), X + 127)
+    for r in range(rows):
+        for b in range(blocks):
+            assert codes[r, b, pos[r, b]] == (15 if sign[r, b] < 0 else 7)
+    scaled = w.astype(np.float64) / np.exp2(X)[:, :, None]
+    got = E2M1_VAL[codes]
+    # Nearest by brute force over the 8 magnitudes (saturating above 6).
+    dist = np.abs(np.abs(np.minimum(np.abs(scaled), 6.0))[..., None] - np.abs(E2M1_VAL[:8]))
+    assert np.all(np.abs(np.abs(got) - np.minimum(np.abs(scaled), 6.0)) <= dist.min(axis=-1) + 0.0)
+    assert np.all((got == 0) | (np.sign(got) == np.sign(scaled)))
+
+
+def test_mxfp4_zero_and_neighbouring_blocks(orc):
+    """A zero block (also -0) gets scale byte 0 and zero codes whatever its
+    neighbours hold; a block's scale sees only its own 32 values."""
+    w = np.zeros((1, 128), np.float32)
+    w[0, 31] = 6.0 * 2 ** 20       # last element of block 0
+    w[0, 32:64] = -0.0              # block 1: negative zeros
+    w[0, 64] = 6.0 * 2 ** -20       # first element of block 2
+    codes, scales = orc.quantize_mxfp4(w, 1, 128)
+    np.testing.assert_array_equal(scales, [20 + 127, 0, -20 + 127, 0])
+    assert codes[31] == 7 and codes[64] == 7
+    assert np.all(codes[32:64] == 0) and np.all(codes[96:] == 0)
+
+
+def test_fp8_row_roundtrips_every_e4m3_value(orc):
+    """Rows holding every e4m3 value (both signs, zeros) times 2^k, with amax
+    = 448 * 2^k, quantize with scale 2^k to exactly those codes (-0 as +0) and
+    dequantize back bit for bit."""
+    rng = np.random.default_rng(43)
+    base = np.array(list(range(0, 127)) + list(range(0x80, 0xff)) + [0, 0x80], np.int64)
+    ks = [-20, -3, 1, 5, 17]
+    rows, cols = len(ks), base.size
+    codes = np.stack([rng.permutation(base) for _ in ks])
+    w = (E4M3_VAL[codes] * np.exp2(np.array(ks, np.float64))[:, None]).astype(np.float32)
+    got_codes, got_scales = orc.quantize_fp8(w, rows, cols)
+    np.testing.assert_array_equal(got_scales, np.exp2(np.array(ks, np.float64)).astype(np.float32))
+    np.testing.assert_array_equal(got_codes.reshape(rows, cols), np.where(codes == 0x80, 0, codes))
+    deq = (E4M3_VAL[got_codes.reshape(rows, cols)] * got_scales[:, None].astype(np.float64)).astype(np.float32)
+    np.testing.assert_array_equal(deq, w)
+
+
+def test_fp8_row_error_bound_on_random_rows(orc):
+    """Random rows: scale = fl(amax / 448), the largest element encodes to
+    +-448, and |deq - w| <= 2^-4 |w| + 2^-10 scale (half an ulp of the 3-bit
+    mantissa, or half the subnormal step)."""
+    rng = np.random.default_rng(44)
+    rows, cols = 12, 777
+    w = (rng.standard_normal((rows, cols)) * np.exp2(rng.integers(-30, 30, rows))[:, None]).astype(np.float32)
+    w[3, :] = 0.0
+    codes, scales = orc.quantize_fp8(w, rows, cols)
+    codes = codes.reshape(rows, cols)
+    amax = np.abs(w).max(axis=1)
+    want = np.where(amax > 0, amax / np.float32(448.0), np.float32(1.0)).astype(np.float32)
+    np.testing.assert_array_equal(scales, want)
+    assert np.all(codes[3] == 0)
+    for r in range(rows):
+        if amax[r] > 0:
+            assert codes[r, np.argmax(np.abs(w[r]))] & 0x7f == 0x7e
+    deq = E4M3_VAL[codes] * scales[:, None].astype(np.float64)
+    err = np.abs(deq - w.astype(np.float64))
+    assert np.all(err <= 2.0 ** -4 * np.abs(w) * (1 + 1e-6) + 2.0 ** -10 * scales[:, None])
+
+
+def _bf16_exact(rng, shape):
+    """Activations n * 2^-7, |n| <= 128: exact in bf16 (8 significant bits)."""
+    n = rng.integers(-128, 129, shape)
+    x = (n * 2.0 ** -7).astype(np.float32)
+    bits = x.view(np.uint32)
+    assert np.all(bits & 0xffff == 0)
+    return n, (bits >> 16).astype(np.uint16)
+
+
+def test_qmatmul_ref_mxfp4_equals_exact_dot(orc):
+    """On exactly representable operands every term and partial sum is exact,
+    so the reference must equal the integer-scaled dot product exactly (and its
+    magnitude the integer sum of |terms|). Weights are packed here, two codes a
+    byte with the even k in the low nibble; swapping the nibbles or shifting
+    the scale byte changes the result."""
+    rng = np.random.default_rng(45)
+    batch, size, rows = 3, 1024, 5
+    n, xb = _bf16_exact(rng, (batch, size))
+    codes = rng.integers(0, 16, (rows, size))
+    X = rng.integers(-4, 5, (rows, size // 32))
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    scales = (X + 127).astype(np.uint8)
+    # w * 2^5 = (2 e2m1) * 2^(X + 4), an integer; x * 2^7 = n.
+    iw = np.rint(2 * E2M1_VAL[codes]).astype(np.int64) * (1 << (np.repeat(X, 32, axis=1) + 4))
+    exact = n.astype(np.int64) @ iw.T
+    exact_mag = np.abs(n).astype(np.int64) @ np.abs(iw).T
+    vectors = [0, 2]
+    out, mag = orc.qmatmul_ref(0, xb, packed, scales, size, rows, vectors, batch)
+    out, mag = out.reshape(batch, rows), mag.reshape(batch, rows)
+    np.testing.assert_array_equal(out[vectors], exact[vectors] / 2.0 ** 12)
+    np.testing.assert_array_equal(mag[vectors], exact_mag[vectors] / 2.0 ** 12)
+    assert np.all(np.isnan(out[1]))
+    swapped = ((packed >> 4) | (packed << 4)).astype(np.uint8)
+    assert not np.array_equal(orc.qmatmul_ref(0, xb, swapped, scales, size, rows, vectors, batch)[0].reshape(batch, rows)[vectors], out[vectors])
+    shifted = (scales + 1).astype(np.uint8)
+    np.testing.assert_array_equal(orc.qmatmul_ref(0, xb, packed, shifted, size, rows, vectors, batch)[0].reshape(batch, rows)[vectors], 2 * out[vectors])
+
+
+def test_qmatmul_ref_fp8_equals_exact_dot(orc):
+    """fp8 weights with power-of-two row scales: the reference equals the
+    integer-scaled dot product exactly; a row's scale applies to that row only."""
+    rng = np.random.default_rng(46)
+    batch, size, rows = 2, 1000, 7
+    n, xb = _bf16_exact(rng, (batch, size))
+    codes = rng.integers(0, 256, (rows, size))
+    codes[(codes & 0x7f) == 0x7f] = 0x12
+    k = rng.integers(-3, 4, rows)
+    scales = np.exp2(k.astype(np.float64)).astype(np.float32)
+    # value * 2^9 is an integer for every e4m3 code; w * 2^12 = that * 2^(k + 3).
+    iv = np.rint(E4M3_VAL[codes] * 2 ** 9).astype(np.int64) * (1 << (k + 3))[:, None]
+    exact = n.astype(np.int64) @ iv.T
+    out, mag = orc.qmatmul_ref(1, xb, codes.astype(np.uint8), scales, size, rows, [0, 1], batch)
+    np.testing.assert_array_equal(out.reshape(batch, rows), exact / 2.0 ** 19)
+    np.testing.assert_array_equal(mag.reshape(batch, rows), (np.abs(n) @ np.abs(iv).T) / 2.0 ** 19)
