@@ -34,6 +34,11 @@ constexpr double kAutoTargetMs = 50.0;
 constexpr int kAutoMinLaunches = 20;
 constexpr int kAutoMaxLaunches = 5000;
 constexpr int kSingleIterations = 20;
+// Per-operation timing: at least this much back-to-back load before the
+// windows (the matrix cores run about 6% slower for the first ~50 ms under
+// load), then this many event windows of K launches, median taken.
+constexpr double kOpWarmMs = 100.0;
+constexpr int kOpWindows = 5;
 
 // Ranges named like the reference's NVTX ranges (llama2c_cuda_graph.cu:164-176).
 void range_push(const char *label) {
@@ -93,12 +98,15 @@ struct Streams {
   hipStream_t rms = nullptr, soft = nullptr, mm = nullptr;
   hipEvent_t fork = nullptr, soft_done = nullptr, mm_done = nullptr;
   hipEvent_t t0 = nullptr, t1 = nullptr;
+  hipEvent_t marks[kOpWindows + 1] = {};
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   ~Streams() {
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
     for (hipEvent_t e : {fork, soft_done, mm_done, t0, t1})
+      if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : marks)
       if (e) (void)hipEventDestroy(e);
     for (hipStream_t s : {rms, soft, mm})
       if (s) (void)hipStreamDestroy(s);
@@ -412,18 +420,34 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
     softmax->assign(h_softmax.ptr, h_softmax.ptr + vec_elems);
     product->assign(h_product.ptr, h_product.ptr + prod_elems);
 
-    // Per-operation timing: K launches of one operation alone on its stream.
+    // Per-operation timing: one operation alone on its own stream. It first
+    // runs back to back for at least kOpWarmMs (synchronized every 32
+    // launches so the queue stays short), then kOpWindows windows of k
+    // launches follow back to back, each between two events; the median
+    // window over k is the launch duration.
     const int k = std::max(5, std::min(launches, 200));
+    for (hipEvent_t &e : st.marks)
+      if (!e) HIP_OK(hipEventCreate(&e));
     auto time_op = [&](hipStream_t s, auto &&op) {
-      op(s);  // one untimed launch
-      HIP_OK(hipStreamSynchronize(s));
-      HIP_OK(hipEventRecord(st.t0, s));
-      for (int i = 0; i < k; ++i) op(s);
-      HIP_OK(hipEventRecord(st.t1, s));
-      HIP_OK(hipEventSynchronize(st.t1));
-      float ms = 0.0f;
-      HIP_OK(hipEventElapsedTime(&ms, st.t0, st.t1));
-      return 1000.0 * ms / k;
+      const auto warm_start = std::chrono::steady_clock::now();
+      do {
+        for (int i = 0; i < 32; ++i) op(s);
+        HIP_OK(hipStreamSynchronize(s));
+      } while (ms_since(warm_start) < kOpWarmMs);
+      HIP_OK(hipEventRecord(st.marks[0], s));
+      for (int w = 0; w < kOpWindows; ++w) {
+        for (int i = 0; i < k; ++i) op(s);
+        HIP_OK(hipEventRecord(st.marks[w + 1], s));
+      }
+      HIP_OK(hipEventSynchronize(st.marks[kOpWindows]));
+      double window_us[kOpWindows];
+      for (int w = 0; w < kOpWindows; ++w) {
+        float ms = 0.0f;
+        HIP_OK(hipEventElapsedTime(&ms, st.marks[w], st.marks[w + 1]));
+        window_us[w] = 1000.0 * ms / k;
+      }
+      std::sort(window_us, window_us + kOpWindows);
+      return window_us[kOpWindows / 2];
     };
     range_push("llama2c.kernels");
     if (mm == Matmul::kFused) {
@@ -471,7 +495,8 @@ std::string result_line(const Options &o, const RunResult &r, const Validation &
       "device=%s arch=%s cus=%d rms_us=%.3f rms_gbps=%.1f rms_hbm_frac=%.4f softmax_us=%.3f "
       "softmax_gbps=%.1f softmax_hbm_frac=%.4f matmul_us=%.3f matmul_gbps=%.1f matmul_tflops=%.3f "
       "matmul_bound=%s matmul_frac=%.4f rms_max_rel_err=%.3e softmax_max_rel_err=%.3e "
-      "product_max_rel_err=%.3e product_max_tol_ratio=%.3e check_vectors=%zu strict_valid=%d",
+      "product_max_rel_err=%.3e product_max_tol_ratio=%.3e check_vectors=%zu strict_valid=%d "
+      "matmul_within_iter=%d",
       o.graph ? "graph" : "direct", matmul_name(o.matmul), r.launches, o.batch, o.size, o.rows,
       o.repeats, o.copy_outputs ? 1 : 0, o.warmup_ms, r.warmup_iterations, r.gpu_ms, gpu_ms_per_iter,
       kSingleIterations, r.single_us, r.wall_ms, r.wall_ms / r.launches, r.submit_us,
@@ -485,7 +510,8 @@ std::string result_line(const Options &o, const RunResult &r, const Validation &
       gbps(r.softmax) / kHbmPeakGbps, r.matmul.us, gbps(r.matmul), mm_tflops,
       batched ? "mfma" : "hbm", mm_frac, v.rms_max_rel_error, v.softmax_max_rel_error,
       v.product_max_rel_error, v.product_max_ratio,
-      batched ? v.product.sampled_batch_rows.size() : static_cast<size_t>(1), strict_valid ? 1 : 0);
+      batched ? v.product.sampled_batch_rows.size() : static_cast<size_t>(1), strict_valid ? 1 : 0,
+      r.matmul.us <= gpu_ms_per_iter * 1000.0 ? 1 : 0);
   std::string line = buf;
   // Device names may contain spaces; keep the line space-separated key=value.
   const size_t d = line.find(" device=");
