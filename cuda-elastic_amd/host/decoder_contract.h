@@ -16,7 +16,7 @@
 #include <thread>
 #include <vector>
 
-#include "lp_harness.h"
+#include "app_protocol.h"
 
 namespace l2c_decoder {
 
@@ -255,13 +255,13 @@ using PinnedArray = std::unique_ptr<T, HipHostFree>;
 template <typename T>
 DeviceArray<T> device_array(size_t count) {
   void *p = nullptr;
-  LP_HIP(hipMalloc(&p, count * sizeof(T)));
+  APP_HIP(hipMalloc(&p, count * sizeof(T)));
   return DeviceArray<T>(static_cast<T *>(p));
 }
 template <typename T>
 PinnedArray<T> pinned_array(size_t count) {
   void *p = nullptr;
-  LP_HIP(hipHostMalloc(&p, count * sizeof(T), hipHostMallocDefault));
+  APP_HIP(hipHostMalloc(&p, count * sizeof(T), hipHostMallocDefault));
   return PinnedArray<T>(static_cast<T *>(p));
 }
 

@@ -28,7 +28,7 @@
 #include "../../include/l2c_harness.h"
 #include "decoder_contract.h"
 #include "lowprec_reference.h"
-#include "lp_harness.h"
+#include "app_protocol.h"
 #include "parallel.h"
 
 namespace {
@@ -59,35 +59,31 @@ struct Operand {
   size_t code_bytes = 0, scale_bytes = 0, wide_count = 0;
 };
 
-class LowprecWorkload final : public lp::Workload {
+class LowprecWorkload final : public appproto::Application {
  public:
   LowprecWorkload(int lowprec_case, long long batch, long long width, long long vocab, long long steps, int fixture,
                   int fault = 0)
       : c_(lowprec_case), d_{batch, width, vocab, steps}, fixture_(fixture), fault_(fault) {}
 
-  std::string identity() const override {
-    return std::string("blackwell-experiments/lowprec-decoder-classifier/") + case_name(c_);
-  }
-
-  lp::JsonObject dimensions() const override {
-    using lp::json::integer;
-    return {{"batch", integer(d_.batch)},
-            {"width", integer(d_.width)},
-            {"vocab", integer(d_.vocab)},
-            {"steps", integer(d_.steps)},
-            {"fixture", integer(fixture_)},
-            {"case", lp::json::quote(case_name(c_))},
-            {"generated_tokens", integer(d_.batch * d_.steps)},
-            {"classifier_macs_per_step", integer(d_.batch * d_.vocab * d_.width)}};
-  }
-
-  std::string application_scope() const override {
-    return "prompt upload (pinned H2D), token reset, every step (rmsnorm, activation conversion with scale "
-           "generation, classifier contraction, softmax+argmax with on-device token feedback), generated-token "
-           "download; converted weights resident from setup";
-  }
-  std::string compute_scope() const override {
-    return "token reset and every step (rmsnorm, activation conversion, classifier contraction, softmax+argmax)";
+  appproto::AppInfo info() const override {
+    using appproto::Json;
+    appproto::AppInfo i;
+    i.identity = std::string("blackwell-experiments/lowprec-decoder-classifier/") + case_name(c_);
+    i.dimensions.add("batch", Json::whole(d_.batch))
+        .add("width", Json::whole(d_.width))
+        .add("vocab", Json::whole(d_.vocab))
+        .add("steps", Json::whole(d_.steps))
+        .add("fixture", Json::whole(fixture_))
+        .add("case", Json::text(case_name(c_)))
+        .add("generated_tokens", Json::whole(d_.batch * d_.steps))
+        .add("classifier_macs_per_step", Json::whole(d_.batch * d_.vocab * d_.width));
+    i.application_scope =
+        "prompt upload (pinned H2D), token reset, every step (rmsnorm, activation conversion with scale "
+        "generation, classifier contraction, softmax+argmax with on-device token feedback), generated-token "
+        "download; converted weights resident from setup";
+    i.compute_scope =
+        "token reset and every step (rmsnorm, activation conversion, classifier contraction, softmax+argmax)";
+    return i;
   }
 
   long long batch() const { return d_.batch; }
@@ -100,12 +96,12 @@ class LowprecWorkload final : public lp::Workload {
   float *logits(long long s) const { return logits_.get() + d_.row_at(0, s); }
   const int *generated() const { return host_generated_.get(); }
   void download_outputs(float *normalized_out, float *logits_out, float *probabilities_out) const {
-    LP_HIP(hipMemcpy(normalized_out, normalized_.get(), d_.activation_count() * 4, hipMemcpyDeviceToHost));
-    LP_HIP(hipMemcpy(logits_out, logits_.get(), d_.row_count() * 4, hipMemcpyDeviceToHost));
-    LP_HIP(hipMemcpy(probabilities_out, probabilities_.get(), d_.row_count() * 4, hipMemcpyDeviceToHost));
+    APP_HIP(hipMemcpy(normalized_out, normalized_.get(), d_.activation_count() * 4, hipMemcpyDeviceToHost));
+    APP_HIP(hipMemcpy(logits_out, logits_.get(), d_.row_count() * 4, hipMemcpyDeviceToHost));
+    APP_HIP(hipMemcpy(probabilities_out, probabilities_.get(), d_.row_count() * 4, hipMemcpyDeviceToHost));
   }
 
-  void setup(hipStream_t stream) override {
+  void prepare(hipStream_t stream) override {
     const size_t model_count = static_cast<size_t>(d_.vocab * d_.width);
     embedding_ = device_array<float>(model_count);
     classifier_ = device_array<float>(model_count);
@@ -120,17 +116,17 @@ class LowprecWorkload final : public lp::Workload {
     host_prompts_ = pinned_array<int>(static_cast<size_t>(d_.batch));
     host_generated_ = pinned_array<int>(d_.token_count());
     if (fixture_ == 0) {
-      LP_L2C(l2c_decoder_init_model(embedding_.get(), classifier_.get(), norm_weight_.get(),
+      APP_L2C(l2c_decoder_init_model(embedding_.get(), classifier_.get(), norm_weight_.get(),
                                     static_cast<int>(d_.width), static_cast<int>(d_.vocab), stream));
     } else {
       host_embedding_.resize(model_count);
       host_classifier_.resize(model_count);
       lowprec::fixture(fixture_, d_.width, d_.vocab, host_embedding_.data(), host_classifier_.data());
       const std::vector<float> ones(static_cast<size_t>(d_.width), 1.0f);
-      LP_HIP(hipMemcpyAsync(embedding_.get(), host_embedding_.data(), model_count * 4, hipMemcpyHostToDevice, stream));
-      LP_HIP(hipMemcpyAsync(classifier_.get(), host_classifier_.data(), model_count * 4, hipMemcpyHostToDevice, stream));
-      LP_HIP(hipMemcpyAsync(norm_weight_.get(), ones.data(), ones.size() * 4, hipMemcpyHostToDevice, stream));
-      LP_HIP(hipStreamSynchronize(stream));
+      APP_HIP(hipMemcpyAsync(embedding_.get(), host_embedding_.data(), model_count * 4, hipMemcpyHostToDevice, stream));
+      APP_HIP(hipMemcpyAsync(classifier_.get(), host_classifier_.data(), model_count * 4, hipMemcpyHostToDevice, stream));
+      APP_HIP(hipMemcpyAsync(norm_weight_.get(), ones.data(), ones.size() * 4, hipMemcpyHostToDevice, stream));
+      APP_HIP(hipStreamSynchronize(stream));
     }
     for (long long b = 0; b < d_.batch; ++b) host_prompts_.get()[b] = static_cast<int>(b % d_.vocab);
     if (c_ != kFp32) {
@@ -138,39 +134,42 @@ class LowprecWorkload final : public lp::Workload {
       for (long long s = 0; s < d_.steps; ++s) activations_.push_back(make_operand(d_.batch));
       if (c_ == kNvfp4) alpha_ = device_array<float>(static_cast<size_t>(d_.steps));
     }
-    LP_HIP(hipStreamSynchronize(stream));
+    APP_HIP(hipStreamSynchronize(stream));
     hipEvent_t start, stop;
-    LP_HIP(hipEventCreate(&start));
-    LP_HIP(hipEventCreate(&stop));
-    LP_HIP(hipEventRecord(start, stream));
+    APP_HIP(hipEventCreate(&start));
+    APP_HIP(hipEventCreate(&stop));
+    APP_HIP(hipEventRecord(start, stream));
     convert_weights(stream);
-    LP_HIP(hipEventRecord(stop, stream));
-    LP_HIP(hipEventSynchronize(stop));
+    APP_HIP(hipEventRecord(stop, stream));
+    APP_HIP(hipEventSynchronize(stop));
     float ms = 0.0f;
-    LP_HIP(hipEventElapsedTime(&ms, start, stop));
+    APP_HIP(hipEventElapsedTime(&ms, start, stop));
     (void)hipEventDestroy(start);
     (void)hipEventDestroy(stop);
-    std::fprintf(stderr, "%s: case %s, fixture %d, weight conversion %.3f ms (setup)\n", lp::app_name().c_str(),
+    std::fprintf(stderr, "%s: case %s, fixture %d, weight conversion %.3f ms (setup)\n", appproto::program(),
                  case_name(c_), fixture_, static_cast<double>(ms));
   }
 
-  void enqueue_application(hipStream_t stream) override {
-    LP_HIP(hipMemcpyAsync(prompts_.get(), host_prompts_.get(), static_cast<size_t>(d_.batch) * sizeof(int),
-                          hipMemcpyHostToDevice, stream));
-    enqueue_compute(stream);
-    LP_HIP(hipMemcpyAsync(host_generated_.get(), generated_.get(), d_.token_count() * sizeof(int),
-                          hipMemcpyDeviceToHost, stream));
+  void enqueue(appproto::Scope scope, hipStream_t stream) override {
+    const bool whole = scope == appproto::Scope::kApplication;
+    if (whole)
+      APP_HIP(hipMemcpyAsync(prompts_.get(), host_prompts_.get(), static_cast<size_t>(d_.batch) * sizeof(int),
+                             hipMemcpyHostToDevice, stream));
+    enqueue_steps(stream);
+    if (whole)
+      APP_HIP(hipMemcpyAsync(host_generated_.get(), generated_.get(), d_.token_count() * sizeof(int),
+                             hipMemcpyDeviceToHost, stream));
   }
 
-  void enqueue_compute(hipStream_t stream) override {
-    LP_HIP(hipMemcpyAsync(tokens_.get(), prompts_.get(), static_cast<size_t>(d_.batch) * sizeof(int),
+  void enqueue_steps(hipStream_t stream) {
+    APP_HIP(hipMemcpyAsync(tokens_.get(), prompts_.get(), static_cast<size_t>(d_.batch) * sizeof(int),
                           hipMemcpyDeviceToDevice, stream));
     const int B = static_cast<int>(d_.batch), W = static_cast<int>(d_.width), V = static_cast<int>(d_.vocab),
               S = static_cast<int>(d_.steps);
     for (int s = 0; s < S; ++s) {
-      LP_L2C(l2c_decoder_rmsnorm(normalized(s), tokens_.get(), embedding_.get(), norm_weight_.get(), W, V, B, stream));
+      APP_L2C(l2c_decoder_rmsnorm(normalized(s), tokens_.get(), embedding_.get(), norm_weight_.get(), W, V, B, stream));
       enqueue_classifier(s, stream);
-      LP_L2C(l2c_decoder_softmax_argmax(probabilities_.get() + d_.row_at(0, s), logits(s), tokens_.get(),
+      APP_L2C(l2c_decoder_softmax_argmax(probabilities_.get() + d_.row_at(0, s), logits(s), tokens_.get(),
                                         generated_.get(), V, B, S, s, stream));
     }
   }
@@ -179,16 +178,16 @@ class LowprecWorkload final : public lp::Workload {
   void enqueue_classifier(int s, hipStream_t stream) {
     const int B = static_cast<int>(d_.batch), W = static_cast<int>(d_.width), V = static_cast<int>(d_.vocab);
     if (c_ == kFp32) {
-      LP_L2C(l2c_matmul(logits(s), normalized(s), classifier_.get(), B, W, V, stream));
+      APP_L2C(l2c_matmul(logits(s), normalized(s), classifier_.get(), B, W, V, stream));
       return;
     }
     Operand &a = activations_[static_cast<size_t>(s)];
     convert(normalized(s), a, alpha_ ? alpha_.get() + s : nullptr, stream);
     if (c_ == kMxfp6)
-      LP_L2C(l2c_matmul_mxfp6(logits(s), a.codes.get(), a.scales.get(), weights_.codes.get(), weights_.scales.get(), B,
+      APP_L2C(l2c_matmul_mxfp6(logits(s), a.codes.get(), a.scales.get(), weights_.codes.get(), weights_.scales.get(), B,
                               W, V, stream));
     else
-      LP_L2C(l2c_matmul_bf16(logits(s), a.wide.get(), weights_.wide.get(), c_ == kNvfp4 ? alpha_.get() + s : nullptr,
+      APP_L2C(l2c_matmul_bf16(logits(s), a.wide.get(), weights_.wide.get(), c_ == kNvfp4 ? alpha_.get() + s : nullptr,
                              B, W, V, stream));
   }
 
@@ -196,9 +195,9 @@ class LowprecWorkload final : public lp::Workload {
     if (c_ != kFp32) convert(classifier_.get(), weights_, nullptr, stream);
   }
 
-  void poison_outputs(hipStream_t stream) override {
+  void scramble_outputs(hipStream_t stream) override {
     auto poison = [&](void *p, size_t bytes) {
-      if (p && bytes) LP_HIP(hipMemsetAsync(p, 0xFF, bytes, stream));
+      if (p && bytes) APP_HIP(hipMemsetAsync(p, 0xFF, bytes, stream));
     };
     poison(prompts_.get(), static_cast<size_t>(d_.batch) * sizeof(int));
     poison(tokens_.get(), static_cast<size_t>(d_.batch) * sizeof(int));
@@ -216,9 +215,9 @@ class LowprecWorkload final : public lp::Workload {
     std::memset(host_generated_.get(), 0xFF, d_.token_count() * sizeof(int));
   }
 
-  void compute_reference() override {
+  void derive_expected() override {
     if (c_ != kFp32) {
-      LP_HIP(hipDeviceSynchronize());
+      APP_HIP(hipDeviceSynchronize());
       const std::vector<float> w = host_weights();
       const Quantized expected = quantize(c_, w.data(), d_.vocab, d_.width);
       const Quantized actual = download(weights_);
@@ -234,7 +233,7 @@ class LowprecWorkload final : public lp::Workload {
     if (c_ == kFp32 && fixture_ == 0) contract_ = std::make_unique<l2c_decoder::Expectation>(d_);
   }
 
-  bool check_outputs() override {
+  bool outputs_match() override {
     download_diagnostics();
     if (fault_ == 3) {
       // Logits as a contraction that ignored alpha would leave them.
@@ -243,13 +242,14 @@ class LowprecWorkload final : public lp::Workload {
     return implementation_check();
   }
 
-  uint64_t output_digest() const override {
-    uint64_t h = lp::fnv1a64(host_generated_.get(), d_.token_count() * sizeof(int));
-    h = lp::fnv1a64(host_normalized_.data(), host_normalized_.size() * 4, h);
-    h = lp::fnv1a64(host_logits_.data(), host_logits_.size() * 4, h);
-    h = lp::fnv1a64(host_probabilities_.data(), host_probabilities_.size() * 4, h);
-    for (const std::vector<uint8_t> &bytes : host_activation_bytes_) h = lp::fnv1a64(bytes.data(), bytes.size(), h);
-    return h;
+  uint64_t outputs_digest() const override {
+    appproto::Digest h;
+    h.add(host_generated_.get(), d_.token_count() * sizeof(int))
+        .add(host_normalized_.data(), host_normalized_.size() * 4)
+        .add(host_logits_.data(), host_logits_.size() * 4)
+        .add(host_probabilities_.data(), host_probabilities_.size() * 4);
+    for (const std::vector<uint8_t> &bytes : host_activation_bytes_) h.add(bytes.data(), bytes.size());
+    return h.value();
   }
 
   // Self-test: the device conversion of a [rows][width] matrix against the host
@@ -257,23 +257,23 @@ class LowprecWorkload final : public lp::Workload {
   bool selftest(const std::vector<float> &m, long long rows) {
     if (c_ == kFp32) return true;
     DeviceArray<float> dm = device_array<float>(m.size());
-    LP_HIP(hipMemcpy(dm.get(), m.data(), m.size() * 4, hipMemcpyHostToDevice));
+    APP_HIP(hipMemcpy(dm.get(), m.data(), m.size() * 4, hipMemcpyHostToDevice));
     Operand o = make_operand(rows);
     DeviceArray<float> other = device_array<float>(1), alpha = device_array<float>(1);
     const float three_quarters = 0.75f;
-    LP_HIP(hipMemcpy(other.get(), &three_quarters, 4, hipMemcpyHostToDevice));
+    APP_HIP(hipMemcpy(other.get(), &three_quarters, 4, hipMemcpyHostToDevice));
     other_decode_override_ = other.get();
     convert(dm.get(), o, alpha.get(), nullptr);
     other_decode_override_ = nullptr;
-    LP_HIP(hipDeviceSynchronize());
+    APP_HIP(hipDeviceSynchronize());
     const Quantized expected = quantize(c_, m.data(), rows, d_.width);
     bool pass = compare("self-test", expected, download(o), rows);
     if (c_ == kNvfp4) {
       float got = 0.0f;
-      LP_HIP(hipMemcpy(&got, alpha.get(), 4, hipMemcpyDeviceToHost));
+      APP_HIP(hipMemcpy(&got, alpha.get(), 4, hipMemcpyDeviceToHost));
       const float want = expected.decode * three_quarters;
       if (got != want) {
-        std::fprintf(stderr, "%s: self-test alpha %.9g, expected %.9g\n", lp::app_name().c_str(),
+        std::fprintf(stderr, "%s: self-test alpha %.9g, expected %.9g\n", appproto::program(),
                      static_cast<double>(got), static_cast<double>(want));
         pass = false;
       }
@@ -315,7 +315,7 @@ class LowprecWorkload final : public lp::Workload {
       o.wide = device_array<uint16_t>(n);
     }
     if (c_ == kMxfp6) {
-      LP_L2C(l2c_mxfp6_bytes(static_cast<int>(rows), static_cast<int>(d_.width), &o.code_bytes, &o.scale_bytes));
+      APP_L2C(l2c_mxfp6_bytes(static_cast<int>(rows), static_cast<int>(d_.width), &o.code_bytes, &o.scale_bytes));
     } else if (c_ == kNvfp4) {
       o.code_bytes = n / 2;
       o.scale_bytes = n / 16;
@@ -332,13 +332,13 @@ class LowprecWorkload final : public lp::Workload {
     const int rows = static_cast<int>(o.rows), W = static_cast<int>(d_.width);
     const long long n = o.rows * d_.width;
     switch (c_) {
-      case kBf16: LP_L2C(l2c_to_bf16_x4(o.wide.get(), x, n, stream)); break;
-      case kMxfp6: LP_L2C(l2c_quantize_mxfp6(o.codes.get(), o.scales.get(), x, rows, W, stream)); break;
+      case kBf16: APP_L2C(l2c_to_bf16_x4(o.wide.get(), x, n, stream)); break;
+      case kMxfp6: APP_L2C(l2c_quantize_mxfp6(o.codes.get(), o.scales.get(), x, rows, W, stream)); break;
       case kNvfp4: {
         const float *other = alpha ? (other_decode_override_ ? other_decode_override_ : weights_.tensor.get() + 1)
                                    : nullptr;
-        LP_L2C(l2c_nvfp4_tensor_scales(o.tensor.get(), alpha, other, x, n, partials_.get(), stream));
-        LP_L2C(l2c_quantize_nvfp4(o.codes.get(), o.scales.get(), o.wide.get(), x, o.tensor.get(), rows, W, stream));
+        APP_L2C(l2c_nvfp4_tensor_scales(o.tensor.get(), alpha, other, x, n, partials_.get(), stream));
+        APP_L2C(l2c_quantize_nvfp4(o.codes.get(), o.scales.get(), o.wide.get(), x, o.tensor.get(), rows, W, stream));
         break;
       }
       default: break;
@@ -358,12 +358,12 @@ class LowprecWorkload final : public lp::Workload {
     const size_t n = static_cast<size_t>(o.rows * d_.width);
     q.codes.resize(n);
     if (c_ == kBf16) {
-      LP_HIP(hipMemcpy(q.codes.data(), o.wide.get(), n * 2, hipMemcpyDeviceToHost));
+      APP_HIP(hipMemcpy(q.codes.data(), o.wide.get(), n * 2, hipMemcpyDeviceToHost));
       return q;
     }
     std::vector<uint8_t> bytes(o.code_bytes), scale_bytes(o.scale_bytes);
-    LP_HIP(hipMemcpy(bytes.data(), o.codes.get(), o.code_bytes, hipMemcpyDeviceToHost));
-    LP_HIP(hipMemcpy(scale_bytes.data(), o.scales.get(), o.scale_bytes, hipMemcpyDeviceToHost));
+    APP_HIP(hipMemcpy(bytes.data(), o.codes.get(), o.code_bytes, hipMemcpyDeviceToHost));
+    APP_HIP(hipMemcpy(scale_bytes.data(), o.scales.get(), o.scale_bytes, hipMemcpyDeviceToHost));
     const long long W = d_.width;
     q.scales.resize(static_cast<size_t>(o.rows * (W / (c_ == kMxfp6 ? 32 : 16))));
     if (c_ == kMxfp6) {
@@ -389,19 +389,19 @@ class LowprecWorkload final : public lp::Workload {
     }
     if (c_ == kNvfp4) {
       float ts[2];
-      LP_HIP(hipMemcpy(ts, o.tensor.get(), 8, hipMemcpyDeviceToHost));
+      APP_HIP(hipMemcpy(ts, o.tensor.get(), 8, hipMemcpyDeviceToHost));
       q.decode = ts[1];
       // The bf16 expansion the contraction multiplies must be the exact value
       // of every code and scale.
       std::vector<uint16_t> wide(n);
-      LP_HIP(hipMemcpy(wide.data(), o.wide.get(), n * 2, hipMemcpyDeviceToHost));
+      APP_HIP(hipMemcpy(wide.data(), o.wide.get(), n * 2, hipMemcpyDeviceToHost));
       long long bad = 0;
       for (size_t i = 0; i < n; ++i) {
         const long long r = static_cast<long long>(i) / d_.width, k = static_cast<long long>(i) % d_.width;
         if (bf16_value(wide[i]) != static_cast<double>(dequantized(c_, q, d_.width, r, k))) ++bad;
       }
       if (bad) {
-        std::fprintf(stderr, "%s: %lld bf16 expansion values differ from their codes\n", lp::app_name().c_str(), bad);
+        std::fprintf(stderr, "%s: %lld bf16 expansion values differ from their codes\n", appproto::program(), bad);
         q.decode = NAN;  // fails the comparison
       }
     }
@@ -410,7 +410,7 @@ class LowprecWorkload final : public lp::Workload {
 
   bool compare(const char *what, const Quantized &expected, const Quantized &actual, long long rows) const {
     long long code_errors = 0, scale_errors = 0;
-    const char *app = lp::app_name().c_str();
+    const char *app = appproto::program();
     for (size_t i = 0; i < expected.codes.size(); ++i)
       if (expected.codes[i] != actual.codes[i] && code_errors++ < kReportLimit)
         std::fprintf(stderr, "%s: %s code mismatch row %lld column %lld: expected 0x%x, actual 0x%x\n", app, what,
@@ -433,21 +433,21 @@ class LowprecWorkload final : public lp::Workload {
     host_normalized_.resize(d_.activation_count());
     host_logits_.resize(d_.row_count());
     host_probabilities_.resize(d_.row_count());
-    LP_HIP(hipMemcpy(host_normalized_.data(), normalized_.get(), host_normalized_.size() * 4, hipMemcpyDeviceToHost));
-    LP_HIP(hipMemcpy(host_logits_.data(), logits_.get(), host_logits_.size() * 4, hipMemcpyDeviceToHost));
-    LP_HIP(hipMemcpy(host_probabilities_.data(), probabilities_.get(), host_probabilities_.size() * 4,
+    APP_HIP(hipMemcpy(host_normalized_.data(), normalized_.get(), host_normalized_.size() * 4, hipMemcpyDeviceToHost));
+    APP_HIP(hipMemcpy(host_logits_.data(), logits_.get(), host_logits_.size() * 4, hipMemcpyDeviceToHost));
+    APP_HIP(hipMemcpy(host_probabilities_.data(), probabilities_.get(), host_probabilities_.size() * 4,
                      hipMemcpyDeviceToHost));
     host_activation_bytes_.clear();
     for (const Operand &a : activations_) {
       std::vector<uint8_t> bytes(a.code_bytes + a.scale_bytes + a.wide_count * 2 + (a.tensor ? 8 : 0));
       uint8_t *p = bytes.data();
-      if (a.code_bytes) LP_HIP(hipMemcpy(p, a.codes.get(), a.code_bytes, hipMemcpyDeviceToHost));
+      if (a.code_bytes) APP_HIP(hipMemcpy(p, a.codes.get(), a.code_bytes, hipMemcpyDeviceToHost));
       p += a.code_bytes;
-      if (a.scale_bytes) LP_HIP(hipMemcpy(p, a.scales.get(), a.scale_bytes, hipMemcpyDeviceToHost));
+      if (a.scale_bytes) APP_HIP(hipMemcpy(p, a.scales.get(), a.scale_bytes, hipMemcpyDeviceToHost));
       p += a.scale_bytes;
-      if (a.wide_count) LP_HIP(hipMemcpy(p, a.wide.get(), a.wide_count * 2, hipMemcpyDeviceToHost));
+      if (a.wide_count) APP_HIP(hipMemcpy(p, a.wide.get(), a.wide_count * 2, hipMemcpyDeviceToHost));
       p += a.wide_count * 2;
-      if (a.tensor) LP_HIP(hipMemcpy(p, a.tensor.get(), 8, hipMemcpyDeviceToHost));
+      if (a.tensor) APP_HIP(hipMemcpy(p, a.tensor.get(), 8, hipMemcpyDeviceToHost));
       host_activation_bytes_.push_back(std::move(bytes));
     }
   }
@@ -462,7 +462,7 @@ class LowprecWorkload final : public lp::Workload {
   // spec.json "implementation_check": every stage against an independent host
   // computation from the GPU's own inputs to that stage.
   bool implementation_check() {
-    const char *app = lp::app_name().c_str();
+    const char *app = appproto::program();
     const long long B = d_.batch, W = d_.width, V = d_.vocab, S = d_.steps;
     // 1. Normalized rows against rmsnorm in double of the token the GPU fed back.
     std::atomic<int> reported{0};
@@ -513,7 +513,7 @@ class LowprecWorkload final : public lp::Workload {
           alpha[static_cast<size_t>(s)] = expected.decode * weight_decode_;
           if (s == 0) alpha_host_ = alpha[0];
           float got = 0.0f;
-          LP_HIP(hipMemcpy(&got, alpha_.get() + s, 4, hipMemcpyDeviceToHost));
+          APP_HIP(hipMemcpy(&got, alpha_.get() + s, 4, hipMemcpyDeviceToHost));
           if (got != alpha[static_cast<size_t>(s)]) {
             std::fprintf(stderr, "%s: alpha step %lld %.9g, expected %.9g\n", app, s, static_cast<double>(got),
                          static_cast<double>(alpha[static_cast<size_t>(s)]));
@@ -638,41 +638,42 @@ class LowprecWorkload final : public lp::Workload {
 // (decoder_lowprec.cu:1106-1127; scripts match the messages).
 std::unique_ptr<LowprecWorkload> make_lowprec(int c, long long batch, long long width, long long vocab, long long steps,
                                               long long fixture, long long fault = 0) {
-  using lp::fail;
-  using lp::kExitUsage;
-  if (fixture < 0 || fixture > 3) fail(kExitUsage, "fixture must be 0 (primary model) or 1, 2, 3 (got %lld)", fixture);
-  if (batch < 1 || batch > (1LL << 20)) fail(kExitUsage, "batch must be in [1, 1048576] (got %lld)", batch);
-  if (width < 2 || width > (1LL << 24) - 16) fail(kExitUsage, "width must be in [2, 16777200] (got %lld)", width);
+  using appproto::abort_run;
+  using appproto::kUsage;
+  if (fixture < 0 || fixture > 3) abort_run(kUsage, "fixture must be 0 (primary model) or 1, 2, 3 (got %lld)", fixture);
+  if (batch < 1 || batch > (1LL << 20)) abort_run(kUsage, "batch must be in [1, 1048576] (got %lld)", batch);
+  if (width < 2 || width > (1LL << 24) - 16) abort_run(kUsage, "width must be in [2, 16777200] (got %lld)", width);
   if (vocab < 2 || vocab > width)
-    fail(kExitUsage, "vocab must satisfy 2 <= vocab <= width (got %lld, %lld)", vocab, width);
-  if (steps < 2 || steps > 1024) fail(kExitUsage, "steps must be in [2, 1024] (got %lld)", steps);
+    abort_run(kUsage, "vocab must satisfy 2 <= vocab <= width (got %lld, %lld)", vocab, width);
+  if (steps < 2 || steps > 1024) abort_run(kUsage, "steps must be in [2, 1024] (got %lld)", steps);
   const long long max_fault = c == kNvfp4 ? 3 : c == kMxfp6 ? 2 : c == kBf16 ? 1 : 0;
   if (fault < 0 || fault > max_fault)
-    fail(kExitUsage, "fault must be in [0, %lld] for case %s (got %lld)", max_fault, case_name(c), fault);
+    abort_run(kUsage, "fault must be in [0, %lld] for case %s (got %lld)", max_fault, case_name(c), fault);
   if (c != kFp32 && (width % 128 != 0 || vocab % 4 != 0))
-    fail(kExitUsage, "low precision cases need width %% 128 == 0 and vocab %% 4 == 0 (got width %lld, vocab %lld)",
+    abort_run(kUsage, "low precision cases need width %% 128 == 0 and vocab %% 4 == 0 (got width %lld, vocab %lld)",
          width, vocab);
   const double gib = static_cast<double>(1LL << 30);
   const double device = 4.0 * (2.0 * static_cast<double>(vocab) * width) +
                         4.0 * static_cast<double>(steps) * batch * (static_cast<double>(width) + 2.0 * vocab) +
                         2.0 * (static_cast<double>(vocab) + steps * static_cast<double>(batch)) * width;
   if (device > kDeviceLimitGiB * gib)
-    fail(kExitUsage, "dimensions need %.1f GiB of device memory (limit %.0f)", device / gib, kDeviceLimitGiB);
+    abort_run(kUsage, "dimensions need %.1f GiB of device memory (limit %.0f)", device / gib, kDeviceLimitGiB);
   return std::make_unique<LowprecWorkload>(c, batch, width, vocab, steps, static_cast<int>(fixture),
                                            static_cast<int>(fault));
 }
 
 int g_case = kFp32;
 
-std::unique_ptr<lp::Workload> make_workload(lp::Options &options) {
-  const long long fixture = options.take_int("fixture", 0);
+std::unique_ptr<appproto::Application> make_workload(const std::string &preset, appproto::Settings &settings,
+                                                     appproto::Assets &) {
+  const long long fixture = settings.integer("fixture", 0);
   const bool dense = fixture != 0;
-  const long long batch = options.take_int("batch", dense ? kFixtureBatch : kLargeBatch);
-  const long long width = options.take_int("width", dense ? kFixtureWidth : kLargeWidth);
-  const long long vocab = options.take_int("vocab", dense ? kFixtureVocab : kLargeVocab);
-  const long long steps = options.take_int("steps", kLargeSteps);
-  const long long fault = options.take_int("fault", 0);
-  if (options.preset != "large") return nullptr;
+  const long long batch = settings.integer("batch", dense ? kFixtureBatch : kLargeBatch);
+  const long long width = settings.integer("width", dense ? kFixtureWidth : kLargeWidth);
+  const long long vocab = settings.integer("vocab", dense ? kFixtureVocab : kLargeVocab);
+  const long long steps = settings.integer("steps", kLargeSteps);
+  const long long fault = settings.integer("fault", 0);
+  if (preset != "large") return nullptr;
   return make_lowprec(g_case, batch, width, vocab, steps, fixture, fault);
 }
 
@@ -733,46 +734,48 @@ int run_selftest(int c) {
   const long long rows = 130, width = 256;
   auto workload = make_lowprec(c, rows, width, 128, 2, 0);
   hipStream_t stream;
-  LP_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
-  workload->setup(stream);
+  APP_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+  workload->prepare(stream);
   const bool pass = workload->selftest(crafted(rows, width), rows);
   (void)hipStreamDestroy(stream);
   std::printf("%s: %s quantizer self-test\n", pass ? "PASS" : "FAIL", case_name(c));
-  return pass ? lp::kExitPass : lp::kExitMismatch;
+  return pass ? appproto::kPass : appproto::kMismatch;
 }
 
 // ---------------------------------------------------------------------------
 // --accuracy (spec.json "accuracy"): the primary model and the three fixtures.
-std::string metrics_json(const ErrorMetrics &m) {
-  using namespace lp::json;
-  return render({{"rows", integer(m.rows)},
-                 {"max_abs_error", number(m.max_abs_error)},
-                 {"normalized_rms_error", number(m.normalized_rms_error)},
-                 {"max_abs_probability_error", number(m.max_abs_probability_error)},
-                 {"mean_total_variation", number(m.mean_total_variation)},
-                 {"top1_agree", integer(m.top1_agree)}});
+appproto::Json metrics_json(const ErrorMetrics &m) {
+  using appproto::Json;
+  Json j = Json::object();
+  j.add("rows", Json::whole(m.rows))
+      .add("max_abs_error", Json::real(m.max_abs_error))
+      .add("normalized_rms_error", Json::real(m.normalized_rms_error))
+      .add("max_abs_probability_error", Json::real(m.max_abs_probability_error))
+      .add("mean_total_variation", Json::real(m.mean_total_variation))
+      .add("top1_agree", Json::whole(m.top1_agree));
+  return j;
 }
 
-std::string accuracy_dataset(int c, int fixture, hipStream_t stream, double *weight_ms) {
-  using namespace lp::json;
+appproto::Json accuracy_dataset(int c, int fixture, hipStream_t stream, double *weight_ms) {
+  using appproto::Json;
   auto w = fixture == 0 ? make_lowprec(c, kLargeBatch, kLargeWidth, kLargeVocab, kLargeSteps, 0)
                         : make_lowprec(c, kFixtureBatch, kFixtureWidth, kFixtureVocab, kLargeSteps, fixture);
   LowprecWorkload &d = *w;
-  d.setup(stream);
-  LP_HIP(hipStreamSynchronize(stream));
+  d.prepare(stream);
+  APP_HIP(hipStreamSynchronize(stream));
   const long long B = d.batch(), W = d.width(), V = d.vocab(), S = d.steps();
   if (weight_ms) {
     std::vector<double> times;
     hipEvent_t start, stop;
-    LP_HIP(hipEventCreate(&start));
-    LP_HIP(hipEventCreate(&stop));
+    APP_HIP(hipEventCreate(&start));
+    APP_HIP(hipEventCreate(&stop));
     for (int i = 0; i < 5; ++i) {
-      LP_HIP(hipEventRecord(start, stream));
+      APP_HIP(hipEventRecord(start, stream));
       d.convert_weights(stream);
-      LP_HIP(hipEventRecord(stop, stream));
-      LP_HIP(hipEventSynchronize(stop));
+      APP_HIP(hipEventRecord(stop, stream));
+      APP_HIP(hipEventSynchronize(stop));
       float ms = 0.0f;
-      LP_HIP(hipEventElapsedTime(&ms, start, stop));
+      APP_HIP(hipEventElapsedTime(&ms, start, stop));
       times.push_back(ms);
     }
     (void)hipEventDestroy(start);
@@ -789,11 +792,11 @@ std::string accuracy_dataset(int c, int fixture, hipStream_t stream, double *wei
     return row.data();
   };
   for (long long b = 0; b < B; ++b) rmsnorm_float(embedding(b % V), W, &activations[static_cast<size_t>(b * W)]);
-  LP_HIP(hipMemcpyAsync(d.normalized(0), activations.data(), activations.size() * 4, hipMemcpyHostToDevice, stream));
+  APP_HIP(hipMemcpyAsync(d.normalized(0), activations.data(), activations.size() * 4, hipMemcpyHostToDevice, stream));
   d.enqueue_classifier(0, stream);
-  LP_HIP(hipStreamSynchronize(stream));
+  APP_HIP(hipStreamSynchronize(stream));
   std::vector<float> logits(static_cast<size_t>(B * V));
-  LP_HIP(hipMemcpy(logits.data(), d.logits(0), logits.size() * 4, hipMemcpyDeviceToHost));
+  APP_HIP(hipMemcpy(logits.data(), d.logits(0), logits.size() * 4, hipMemcpyDeviceToHost));
   std::vector<double> reference(static_cast<size_t>(B * V)), actual(logits.begin(), logits.end());
   l2c_host::parallel_ranges(static_cast<size_t>(B), threads(), [&](size_t b0, size_t b1, size_t) {
     for (long long b = static_cast<long long>(b0); b < static_cast<long long>(b1); ++b) {
@@ -813,9 +816,9 @@ std::string accuracy_dataset(int c, int fixture, hipStream_t stream, double *wei
   const ErrorMetrics classifier = compare_logits(reference, actual, B, V);
 
   // A complete decode (one application-scope invocation).
-  d.poison_outputs(stream);
-  d.enqueue_application(stream);
-  LP_HIP(hipStreamSynchronize(stream));
+  d.scramble_outputs(stream);
+  d.enqueue(appproto::Scope::kApplication, stream);
+  APP_HIP(hipStreamSynchronize(stream));
   std::vector<int> expected(static_cast<size_t>(B * S));
   if (fixture == 0) {
     for (long long b = 0; b < B; ++b)
@@ -840,34 +843,40 @@ std::string accuracy_dataset(int c, int fixture, hipStream_t stream, double *wei
     });
   }
   long long agree = 0;
-  std::string per_step = "[";
+  Json per_step = Json::list();
   for (long long s = 0; s < S; ++s) {
     long long n = 0;
     for (long long b = 0; b < B; ++b) n += d.generated()[b * S + s] == expected[static_cast<size_t>(b * S + s)];
     agree += n;
-    per_step += (s ? ", " : "") + integer(n);
+    per_step.push(Json::whole(n));
   }
-  per_step += "]";
-  lp::JsonObject out = {
-      {"dataset", quote(fixture == 0 ? "primary" : "fixture" + std::to_string(fixture))},
-      {"batch", integer(B)}, {"width", integer(W)}, {"vocab", integer(V)}, {"steps", integer(S)},
-      {"classifier_error", metrics_json(classifier)},
-      {"tokens", render({{"agree", integer(agree)}, {"total", integer(B * S)}, {"per_step_agree", per_step},
-                         {"reference", quote(fixture == 0 ? "analytic progression" : "double host decode")}})}};
+  Json tokens = Json::object();
+  tokens.add("agree", Json::whole(agree))
+      .add("total", Json::whole(B * S))
+      .add("per_step_agree", std::move(per_step))
+      .add("reference", Json::text(fixture == 0 ? "analytic progression" : "double host decode"));
+  Json out = Json::object();
+  out.add("dataset", Json::text(fixture == 0 ? "primary" : "fixture" + std::to_string(fixture)))
+      .add("batch", Json::whole(B))
+      .add("width", Json::whole(W))
+      .add("vocab", Json::whole(V))
+      .add("steps", Json::whole(S))
+      .add("classifier_error", metrics_json(classifier))
+      .add("tokens", std::move(tokens));
   if (fixture == 0) {
     const l2c_decoder::Dims dims{B, W, V, S};
     const l2c_decoder::Expectation production(dims);
     std::vector<float> o(dims.activation_count()), l(dims.row_count()), p(dims.row_count());
     d.download_outputs(o.data(), l.data(), p.data());
     std::fprintf(stderr, "%s: production FP32 tolerance check of the %s decode (reported, not required):\n",
-                 lp::app_name().c_str(), case_name(c));
+                 appproto::program(), case_name(c));
     const bool pass = l2c_decoder::verify(dims, production, {d.generated(), o.data(), l.data(), p.data()});
-    out.push_back({"production_fp32_tolerance_pass", boolean(pass)});
+    out.add("production_fp32_tolerance_pass", Json::flag(pass));
   }
   std::fprintf(stderr, "%s: accuracy %s fixture %d: max |error| %.3g, normalized RMS %.3g, max |probability error| "
-               "%.3g, tokens %lld/%lld\n", lp::app_name().c_str(), case_name(c), fixture, classifier.max_abs_error,
+               "%.3g, tokens %lld/%lld\n", appproto::program(), case_name(c), fixture, classifier.max_abs_error,
                classifier.normalized_rms_error, classifier.max_abs_probability_error, agree, B * S);
-  return render(out);
+  return out;
 }
 
 int run_accuracy(int c, int argc, const char *const *argv, std::string *record, bool print) {
@@ -876,60 +885,62 @@ int run_accuracy(int c, int argc, const char *const *argv, std::string *record, 
     const std::string flag = argv[i];
     if (flag == "--accuracy") continue;
     if (flag == "--json-out" && i + 1 < argc) json_out = argv[++i];
-    else lp::fail(lp::kExitUsage, "--accuracy takes only --json-out PATH (got %s)", flag.c_str());
+    else appproto::abort_run(appproto::kUsage, "--accuracy takes only --json-out PATH (got %s)", flag.c_str());
   }
   hipStream_t stream;
-  LP_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+  APP_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
   double weight_ms = 0.0;
-  std::string datasets = "[";
+  appproto::Json datasets = appproto::Json::list();
   for (int fixture = 0; fixture <= 3; ++fixture)
-    datasets += (fixture ? ", " : "") + accuracy_dataset(c, fixture, stream, fixture == 0 ? &weight_ms : nullptr);
-  datasets += "]";
+    datasets.push(accuracy_dataset(c, fixture, stream, fixture == 0 ? &weight_ms : nullptr));
   (void)hipStreamDestroy(stream);
   hipDeviceProp_t prop{};
   int device = 0;
-  LP_HIP(hipGetDevice(&device));
-  LP_HIP(hipGetDeviceProperties(&prop, device));
-  using namespace lp::json;
-  const std::string line =
-      render({{"schema", quote("blackwell_experiments.lowprec_accuracy/1")},
-              {"identity", quote(std::string("blackwell-experiments/lowprec-decoder-classifier/") + case_name(c))},
-              {"case", quote(case_name(c))},
-              {"spec_sha256", quote(kSpecSha256)},
-              {"device", quote(prop.name)},
-              {"weight_conversion_ms_median_of_5", number(weight_ms)},
-              {"datasets", datasets},
-              {"status", quote("accuracy")}});
+  APP_HIP(hipGetDevice(&device));
+  APP_HIP(hipGetDeviceProperties(&prop, device));
+  using appproto::Json;
+  Json result = Json::object();
+  result.add("schema", Json::text("blackwell_experiments.lowprec_accuracy/1"))
+      .add("identity", Json::text(std::string("blackwell-experiments/lowprec-decoder-classifier/") + case_name(c)))
+      .add("case", Json::text(case_name(c)))
+      .add("spec_sha256", Json::text(kSpecSha256))
+      .add("device", Json::text(prop.name))
+      .add("weight_conversion_ms_median_of_5", Json::real(weight_ms))
+      .add("datasets", std::move(datasets))
+      .add("status", Json::text("accuracy"));
+  const std::string line = result.dump();
   if (record) *record = line;
   if (print) std::printf("RESULT %s\n", line.c_str());
   if (!json_out.empty()) {
     FILE *file = std::fopen(json_out.c_str(), "w");
     if (!file || std::fprintf(file, "%s\n", line.c_str()) < 0 || std::fclose(file))
-      lp::fail(lp::kExitUsage, "cannot write %s", json_out.c_str());
+      appproto::abort_run(appproto::kUsage, "cannot write %s", json_out.c_str());
   }
-  return lp::kExitPass;
+  return appproto::kPass;
 }
 
-const lp::Build kBuild{"gfx950", kSpecSha256, "v1", "4a75f8d743ef7fe755822bab0ea0fb78009c145b"};
+const appproto::Provenance kBuild{"gfx950", kSpecSha256, "v1", "4a75f8d743ef7fe755822bab0ea0fb78009c145b"};
+const char kProgram[] = "decoder_lowprec";
 
 // The modes of decoder_lowprec.cu:1414-1420: --accuracy, --selftest, else the
 // loom_private protocol.
 int dispatch(int c, int argc, const char *const *argv, std::string *record, bool print) {
   if (c < kFp32 || c > kNvfp4) {
     std::fprintf(stderr, "lowprec: case must be 0 (fp32), 1 (bf16), 2 (mxfp6) or 3 (nvfp4) (got %d)\n", c);
-    return lp::kExitUsage;
+    return appproto::kUsage;
   }
-  lp::set_app_name("decoder_lowprec");
+  appproto::set_program(kProgram);
   g_case = c;
   try {
     for (int i = 1; i < argc; ++i) {
       if (std::string(argv[i]) == "--accuracy") return run_accuracy(c, argc, argv, record, print);
       if (std::string(argv[i]) == "--selftest") return run_selftest(c);
     }
-  } catch (const lp::Exit &e) {
-    return e.code;
+  } catch (const appproto::Abort &a) {
+    std::fprintf(stderr, "%s: %s\n", appproto::program(), a.what());
+    return a.code();
   }
-  return lp::run_main(argc, argv, make_workload, kBuild, record, print);
+  return appproto::run_protocol(kProgram, argc, argv, make_workload, kBuild, record, print);
 }
 
 }  // namespace

@@ -4,6 +4,7 @@ every run exit 0 and valid=1), extended to this build's variants, and the
 dump compare flow of llama2c/compare_sota.sh:41-71 (graph, direct and fused
 dumps on identical inputs must match within the oracle tolerances), with the
 oracle re-checking every dump independently."""
+import dataclasses
 import math
 import os
 
@@ -37,15 +38,30 @@ def test_check_matrix_small(l2c, shape, inputs, variant):
             assert rec["launches"] >= 20 and rec["inputs"] == inputs.split("=")[0]
 
 
-@pytest.mark.parametrize("variant", ["coalesced", "batched", "fused", "naive"])
-def test_sheet_shape(l2c, variant):
-    """The sheet shape 1024 x 16384 x 8192 in graph and direct mode."""
-    for mode, copies in (("graph", "nocopy"), ("direct", "copy")):
-        args = [mode, 3, 1024, 16384, 8192, 1, 1, copies, variant, "random=1"]
-        print("case", " ".join(map(str, args)), flush=True)
-        code, rec, raw = run(l2c, args)
-        assert code == 0 and rec["valid"] == 1, raw
-        assert rec["strict_valid"] == 1, raw
+def _sheet_cases():
+    from l2c import matrix
+    return [dataclasses.replace(c, launches="3") for c in matrix.check_plan(shapes=[matrix.SHEET])]
+
+
+@pytest.mark.parametrize("case", _sheet_cases(), ids=lambda c: f"{c.label}/{c.inputs}")
+def test_sheet_shape_check_matrix(l2c, case):
+    """The reference's check matrix at the sheet shape 1024 x 16384 x 8192:
+    deterministic, random=1 and random=2 inputs x every variant x graph and
+    direct x copy and nocopy (llama2c/Makefile:44-56)."""
+    print("case", " ".join(case.argv()), flush=True)
+    code, rec, raw = run(l2c, case.argv())
+    assert code == 0 and rec["valid"] == 1, raw
+    assert rec["strict_valid"] == 1, raw
+
+
+def test_sheet_shape_fullcheck(l2c):
+    """The batched product at the sheet shape validated on every one of its
+    1024 x 8192 elements (the fullcheck token), not on sampled batch rows."""
+    args = ["graph", 3, 1024, 16384, 8192, 1, 1, "nocopy", "batched", "random=2", "fullcheck"]
+    print("case", " ".join(map(str, args)), flush=True)
+    code, rec, raw = run(l2c, args)
+    assert code == 0 and rec["valid"] == 1 and rec["strict_valid"] == 1, raw
+    assert rec["check_vectors"] == 1024, raw
 
 
 @pytest.mark.parametrize("variant,inputs", [("mxfp4", "normal=1"), ("fp8", "normal=2"),
@@ -85,28 +101,33 @@ def _oracle_recheck(orc, dump, mode_name, seed):
     np.testing.assert_array_equal(dump["product_reference"], refv)
 
 
-@pytest.mark.parametrize("shape", [(64, 1000, 300), (33, 1001, 77), (1024, 16384, 8192)],
-                         ids=lambda s: "x".join(map(str, s)))
-@pytest.mark.parametrize("inputs", ["deterministic", "random=1", "random=2", "random=3"])
-def test_compare_flow(l2c, orc, tmp_path, shape, inputs):
-    if shape[0] == 1024 and inputs not in ("random=1", "deterministic"):
-        pytest.skip("the sheet shape runs two input sets to bound the run time")
-    batch, size, rows = shape
+def _compare_groups():
+    from l2c import matrix
+    return matrix.compare_plan(copies=("nocopy",)) + matrix.compare_plan(
+        shapes=[(64, 1000, 300), (33, 1001, 77)], inputs=["random=1"], copies=("copy",))
+
+
+@pytest.mark.parametrize("group", _compare_groups(),
+                         ids=lambda g: f"{g[0].batch}x{g[0].size}x{g[0].rows}-{g[0].copies}-{g[0].inputs}")
+def test_compare_flow(l2c, orc, tmp_path, group):
+    """Graph, direct, fused and naive dumps on identical inputs agree within the
+    oracle tolerances (llama2c/compare_sota.sh:41-71), and at the small shapes
+    the oracle re-checks every dump from regenerated inputs."""
+    from l2c import matrix
     dumps = []
-    for label, mode, variant in (("graph", "graph", "coalesced"), ("direct", "direct", "coalesced"),
-                                 ("fused", "graph", "fused"), ("naive", "direct", "naive")):
-        path = str(tmp_path / f"{label}.bin")
-        args = [mode, 3, batch, size, rows, 1, 1, "nocopy", variant, inputs, f"--dump={path}"]
-        print("case", " ".join(map(str, args)), flush=True)
-        code, rec, raw = run(l2c, args)
-        assert code == 0 and rec["valid"] == 1, raw
+    for case in group:
+        path = str(tmp_path / f"{case.label}.bin")
+        print("case", " ".join(case.argv(path)), flush=True)
+        o = matrix.execute(case, dump=path)
+        assert o.ok, o.raw
         dumps.append(path)
     code, out = l2c.compare_dumps(dumps)
     print(out)
     assert code == 0, out
+    inputs = group[0].inputs
     name = inputs.split("=")[0]
     seed = int(inputs.split("=")[1]) if "=" in inputs else 0
-    if batch * size <= 1 << 20:
+    if group[0].batch * group[0].size <= 1 << 20:
         for p in dumps:
             _oracle_recheck(orc, orc.read_dump(p), name, seed)
 

@@ -77,3 +77,23 @@ def test_small_sweep_on_gpu(torch_gpu, tmp_path):
     assert [r["mode"] for r in rows] == ["direct", "graph", "direct", "graph"]
     _, summary = sweep.write_speedup(path)
     assert len(summary) == 2 and all(s["gpu_speedup"] > 0 for s in summary)
+
+
+def test_check_and_compare_plans():
+    """The run plans restate the reference's matrices: check = 3 shapes x
+    {deterministic, random=1, random=2} x 4 variants x graph/direct x
+    copy/nocopy (llama2c/Makefile:44-56); compare = one group of graph /
+    direct / fused / naive runs per shape x input set (compare_sota.sh:41-71)."""
+    from l2c import matrix
+    plan = matrix.check_plan()
+    assert len(plan) == 3 * 3 * 4 * 2 * 2 and len(set(plan)) == len(plan)
+    assert {(c.batch, c.size, c.rows, c.repeats) for c in plan} == set(matrix.CHECK_SHAPES)
+    assert {c.variant for c in plan} == {"coalesced", "naive", "fused", "batched"}
+    assert plan[0].argv() == ["graph", "auto", "64", "1000", "300", "1", "1", "nocopy", "coalesced",
+                              "deterministic"]
+    groups = matrix.compare_plan()
+    assert len(groups) == 3 * 4
+    for g in groups:
+        assert [c.label for c in g] == ["graph", "direct", "fused", "naive"]
+        assert len({(c.batch, c.size, c.rows, c.inputs, c.copies) for c in g}) == 1
+    assert groups[0][0].argv("/tmp/x.bin")[-1] == "--dump=/tmp/x.bin"
