@@ -1,0 +1,428 @@
+// Block-scaled quantized-weight contraction on the gfx950 scaled matrix cores:
+//   out[b][r] = sum_k deq(Xq)[b][k] * deq(W)[r][k],
+// where Xq is the bf16 activations quantized on the device to MXFP8 (E4M3
+// codes, one UE8M0 scale per 32 k) and W the same quantized weights that
+// l2c_matmul_q takes: MXFP4 (E2M1 codes, UE8M0 scale per 32 k) or E4M3 codes
+// with one fp32 scale per row. The products are exact; accumulation is the
+// matrix core's FP32.
+//
+// Activation quantizer (HBM bound; per element 2 B read, 1 B + 1/32 B
+// written): one lane per 8 consecutive values (one 16-byte load), four lanes
+// per 32-value block, the block maximum reduced across the four lanes. The
+// shared exponent is the smallest X with amax <= 448 * 2^X, read off amax's
+// fields: floor(log2 amax) - 8, plus one when amax's significand exceeds
+// 1.75 (448 = 1.75 * 2^8), clamped below at -127; elements are
+// E4M3(v * 2^-X), nearest-even (l2c_formats.h e4m3_code), never beyond 448.
+// Workspace layout: codes row-major [batch][cols]; at offset
+// round_up(batch * cols, 256) the scales in k-step tiles [cols / 128][Bp][4]
+// (Bp = batch rounded up to 4; byte j of a row's word is block j of the
+// 128-k step; padding rows hold 0), so one step's scale words of a 256-row
+// tile are 1 KB contiguous.
+//
+// Contraction kernel:
+//  * v_mfma_scale_f32_32x32x64_f8f6f4, A = activations in format 0 (E4M3,
+//    8 VGPRs a lane: 32 codes), B = weights in format 4 (E2M1, 4 VGPRs: 32
+//    codes) or 0 (E4M3). Lane l supplies row l % 32 of its operand; lane half
+//    h = l / 32 supplies the scale byte of the instruction's k-block
+//    [32 h, 32 h + 32). Where each code sits in k differs by format
+//    (measured on MI355X, operands and outputs fitted against the oracle's
+//    arithmetic; only this placement fits, to fp32 rounding): an E2M1
+//    operand's half h holds k [32 h, 32 h + 32) in order; an E4M3 operand's
+//    half h holds k [16 h, 16 h + 16) in VGPRs 0-3 and k [32 + 16 h,
+//    32 + 16 h + 16) in VGPRs 4-7. So an E4M3 lane takes the h-th 16-value
+//    half of each of the instruction's two blocks, an E2M1 lane one whole
+//    block. The fp8 weights' block scale is 2^0; their fp32 row scale
+//    multiplies the output.
+//  * Tile 256 (batch) x 128 (rows) x 128 (k per step), 8 wavefronts. Waves w
+//    and w + 4 share a SIMD and a 128 x 64 output sub-tile (4 x 2 blocks of
+//    32 x 32); wave group g = w / 4 takes the MFMA k-slice [64 g, 64 g + 64)
+//    of every step, lane half h block 2 g + h. The two groups' partial sums
+//    are added once at the end through LDS, group 1's before group 0's.
+//  * Staging by LDS DMA (buffer_load ... lds, 16 B a lane) from the row-major
+//    operands: X codes 32 KB a step (32 one-KB instructions, 8 rows of 128 B
+//    each), the X scale words (one instruction), W codes 8 KB (MXFP4, 16 rows
+//    of 64 B an instruction) or 16 KB (fp8), MXFP4 W scales as 4-byte DMAs,
+//    one row a lane. 16-byte chunks of LDS rows are XOR-swizzled by row bits
+//    (128-byte rows: bits 1..3; 64-byte rows: bits 2..3), applied on the
+//    DMA's source side, so 32 lanes reading one chunk of 32 consecutive rows
+//    hit distinct bank groups. Three stages (124 KB MXFP4, 147 KB fp8): step
+//    t's DMA is issued in step t - 2 and waited (vmcnt) before the barrier of
+//    step t - 1, one barrier a step.
+//  * Every access is in bounds by construction: operand rows past the end are
+//    clamped per lane to the last row, scale words past the padded rows to
+//    the last four rows; those rows are computed and never stored.
+//  * Workgroup order is remapped per XCD as in the other contractions.
+#include "l2c_common.h"
+#include "l2c_formats.h"
+#include "../../include/l2c.h"
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_ptr;
+
+constexpr int kBM = 256;
+constexpr int kBN = 128;
+constexpr int kBK = 128;
+constexpr int kThreads = 512;
+constexpr int kStages = 3;
+constexpr int kXcds = 8;
+constexpr int kFmtE4M3 = 0;
+constexpr int kFmtE2M1 = 4;
+constexpr int kExchange = 131072;  // 4 sub-tiles x 8 blocks x 16 values x 64 lanes x 4 B
+
+size_t round256(size_t n) { return (n + 255) / 256 * 256; }
+__host__ __device__ __forceinline__ int padded4(int rows) { return (rows + 3) / 4 * 4; }
+
+template <int FMT>
+struct Geometry {
+  static constexpr bool kMx = FMT == L2C_Q_MXFP4;
+  static constexpr int kXBytes = kBM * kBK;      // 32 KB of X codes
+  static constexpr int kWRow = kMx ? 64 : 128;   // W code bytes per row and step
+  static constexpr int kWBytes = kBN * kWRow;
+  static constexpr int kXS = kXBytes + kWBytes;  // X scale words, 256 x 4 B
+  static constexpr int kWS = kXS + kBM * 4;      // W scale words, 128 x 4 B (MXFP4)
+  static constexpr int kStage = kWS + (kMx ? kBN * 4 : 0);
+  static constexpr int kLds = kStages * kStage > kExchange ? kStages * kStage : kExchange;
+  // DMA instructions a wave issues per step: X codes 4, W codes 1 (MXFP4) or
+  // 2 (fp8), plus the X scales on wave 4 and the W scales on waves 5 and 6.
+  static __device__ __forceinline__ int dma_count(int wave) {
+    return 4 + (kMx ? 1 : 2) + (wave == 4 ? 1 : 0) + (kMx && (wave == 5 || wave == 6) ? 1 : 0);
+  }
+  static __device__ __forceinline__ int wswizzle(int row) { return kMx ? (row >> 2) & 3 : (row >> 1) & 7; }
+};
+static_assert(kStages * Geometry<L2C_Q_FP8>::kStage <= 160 * 1024, "the fp8 stages fit the LDS");
+
+__device__ __forceinline__ int xswizzle(int row) { return (row >> 1) & 7; }
+
+// ---------------------------------------------------------------------------
+// Activation quantizer.
+
+__global__ __launch_bounds__(256) void quantize_mxfp8_kernel(uint8_t *__restrict__ codes,
+                                                             uint8_t *__restrict__ scales,
+                                                             const uint16_t *__restrict__ X, int rows,
+                                                             int rows_padded, int cols) {
+  const int lanes_per_row = cols / 8;  // a multiple of 16 (cols % 128 == 0)
+  const long long id = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (id >= static_cast<long long>(rows_padded) * lanes_per_row) return;  // whole 4-lane groups
+  const int row = static_cast<int>(id / lanes_per_row);
+  const int chunk = static_cast<int>(id % lanes_per_row);
+  const int k0 = 8 * chunk;
+  uint8_t *scale_at = scales + (static_cast<size_t>(k0 / kBK) * rows_padded + row) * 4 + (k0 / 32) % 4;
+  if (row >= rows) {  // padding row of the scale tiles
+    if ((chunk & 3) == 0) *scale_at = 0;
+    return;
+  }
+  const u32x4 raw = *reinterpret_cast<const u32x4 *>(X + static_cast<size_t>(row) * cols + k0);
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(raw[i] << 16);
+    v[2 * i + 1] = __uint_as_float(raw[i] & 0xffff0000u);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  // ceil(log2(amax / 448)): the exponent field less 127 + 8, plus one above a
+  // significand of 1.75 (mantissa field 0x600000); a zero or subnormal
+  // maximum clamps to -127, and the largest field, 254, gives at most 120.
+  const unsigned abits = __float_as_uint(amax);
+  const int x = max(static_cast<int>((abits >> 23) & 0xffu) - 135 + ((abits & 0x7fffffu) > 0x600000u ? 1 : 0), -127);
+  const float inv = __uint_as_float(static_cast<unsigned>(127 - x) << 23);  // 2^-x, exact
+  unsigned packed[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) packed[i / 4] |= l2c::e4m3_code(v[i] * inv) << (8 * (i % 4));
+  *reinterpret_cast<uint2 *>(codes + static_cast<size_t>(row) * cols + k0) = make_uint2(packed[0], packed[1]);
+  if ((chunk & 3) == 0) *scale_at = static_cast<uint8_t>(x + 127);
+}
+
+// ---------------------------------------------------------------------------
+// The contraction.
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads, 1) void scaled_gemm_kernel(float *__restrict__ out,
+                                                                  const uint8_t *__restrict__ Xc,
+                                                                  const uint8_t *__restrict__ Xs,
+                                                                  const uint8_t *__restrict__ Wq,
+                                                                  const void *__restrict__ wscales, int M,
+                                                                  int N, int K) {
+  using G = Geometry<FMT>;
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[G::kLds];
+  int tile = blockIdx.x;
+  const int tiles = gridDim.x;
+  if (tiles % kXcds == 0) tile = (tile % kXcds) * (tiles / kXcds) + tile / kXcds;
+  const int mtiles = (M + kBM - 1) / kBM;
+  const int m0 = (tile % mtiles) * kBM, n0 = (tile / mtiles) * kBN;
+  const int mrows = min(kBM, M - m0), nrows = min(kBN, N - n0);
+  const int Mp = padded4(M);
+  const int tid = threadIdx.x, lane = tid % L2C_WAVE;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / L2C_WAVE);
+  const int g = wave >> 2, p = wave & 3;
+  const int wm = p & 1, wn = p >> 1;
+  const int r = lane % 32, h = lane / 32;
+  const int steps = K / kBK;
+  const int wrb = G::kMx ? K / 2 : K;  // W code bytes per row
+  const int srb = K / 32;              // MXFP4 W scale bytes per row
+  const __amdgpu_buffer_rsrc_t rx =
+      l2c::buffer_rsrc(Xc + static_cast<size_t>(m0) * K, static_cast<uint32_t>(mrows) * K);
+  const __amdgpu_buffer_rsrc_t rxs = l2c::buffer_rsrc(Xs, static_cast<uint32_t>(Mp) * 4 * steps);
+  const __amdgpu_buffer_rsrc_t rw =
+      l2c::buffer_rsrc(Wq + static_cast<size_t>(n0) * wrb, static_cast<uint32_t>(nrows) * wrb);
+  const __amdgpu_buffer_rsrc_t rws =
+      G::kMx ? l2c::buffer_rsrc(static_cast<const uint8_t *>(wscales) + static_cast<size_t>(n0) * srb,
+                                static_cast<uint32_t>(nrows) * srb)
+             : rw;
+
+  // Per-lane DMA sources (the step's k offset is scalar). X: instruction
+  // 8k + wave (k < 4) fills rows 8 (8k + wave) + lane / 8, slot lane % 8 with
+  // chunk slot ^ xswizzle(row). W (MXFP4): instruction `wave` fills rows
+  // 16 wave + lane / 4, slot lane % 4; W (fp8): instructions 8k + wave (k < 2)
+  // as X. X scales (wave 4): lane covers rows 4 lane .. 4 lane + 3. W scales
+  // (waves 5, 6): row 64 (wave - 5) + lane.
+  int xsrc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int row = 8 * (8 * k + wave) + lane / 8;
+    xsrc[k] = min(row, mrows - 1) * K + 16 * ((lane % 8) ^ xswizzle(row));
+  }
+  int wsrc[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if constexpr (G::kMx) {
+      const int row = 16 * wave + lane / 4;
+      wsrc[k] = min(row, nrows - 1) * wrb + 16 * ((lane % 4) ^ G::wswizzle(row));
+    } else {
+      const int row = 8 * (8 * k + wave) + lane / 8;
+      wsrc[k] = min(row, nrows - 1) * wrb + 16 * ((lane % 8) ^ G::wswizzle(row));
+    }
+  }
+  const int xssrc = min(16 * lane, (Mp - m0) * 4 - 16);
+  const int wssrc = min(64 * max(wave - 5, 0) + lane, nrows - 1) * srb;
+
+  auto dma = [&](int stage, int t) __attribute__((always_inline)) {
+    unsigned char *base = lds + stage * G::kStage;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr *)(base + (8 * k + wave) * 1024), 16, xsrc[k], kBK * t,
+                                               0, 0);
+    if constexpr (G::kMx) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + G::kXBytes + wave * 1024), 16, wsrc[0],
+                                               64 * t, 0, 0);
+      if (wave == 5 || wave == 6)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rws, (lds_ptr *)(base + G::kWS + (wave - 5) * 256), 4, wssrc,
+                                                 4 * t, 0, 0);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + G::kXBytes + (8 * k + wave) * 1024), 16,
+                                                 wsrc[k], kBK * t, 0, 0);
+    }
+    if (wave == 4)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rxs, (lds_ptr *)(base + G::kXS), 16, xssrc, Mp * 4 * t + m0 * 4, 0,
+                                               0);
+  };
+  // This wave's DMA of the older of two outstanding steps has landed and its
+  // LDS reads are done; then the workgroup barrier. Nothing is scheduled
+  // across it.
+  const int outstanding = G::dma_count(wave);
+  auto sync = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (outstanding == 5)
+      asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if (outstanding == 6)
+      asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Fragments of lane (r, h) for the instruction over the step's blocks
+  // 2 g and 2 g + 1 (16-byte chunks 4 g .. 4 g + 3 of a 128-byte fp8 row,
+  // chunks 2 g, 2 g + 1 of a 64-byte MXFP4 row): X rows wm * 128 + 32 i + r,
+  // chunks 4 g + h and 4 g + 2 + h (the h-th halves of both blocks); W rows
+  // wn * 64 + 32 j + r, fp8 the same two chunks, MXFP4 chunk 2 g + h (block
+  // 2 g + h whole). Scale bytes: block 2 g + h of the row's word for both
+  // operands. The swizzle of row + 32 equals that of row.
+  const int blk = 2 * g + h;
+  const int xsw = xswizzle(r);
+  const int xa = (wm * 128 + r) * 128;
+  const int xc0 = 16 * ((4 * g + h) ^ xsw), xc1 = 16 * ((4 * g + 2 + h) ^ xsw);
+  const int wr0 = wn * 64 + r;
+  const int wsw = G::wswizzle(wr0);
+  const int wa = G::kXBytes + wr0 * G::kWRow;
+  const int wc0 = G::kMx ? 16 * (blk ^ wsw) : 16 * ((4 * g + h) ^ wsw);
+  const int wc1 = 16 * ((4 * g + 2 + h) ^ wsw);
+  const int shift = 8 * blk;
+  u32x4 fa[4][2], fb[2][2];
+  unsigned sa[4], sb[2];
+  auto read = [&](int stage) __attribute__((always_inline)) {
+    const unsigned char *base = lds + stage * G::kStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fa[i][0] = *reinterpret_cast<const u32x4 *>(base + xa + 4096 * i + xc0);
+      fa[i][1] = *reinterpret_cast<const u32x4 *>(base + xa + 4096 * i + xc1);
+      sa[i] = *reinterpret_cast<const unsigned *>(base + G::kXS + (wm * 128 + 32 * i + r) * 4) >> shift;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      fb[j][0] = *reinterpret_cast<const u32x4 *>(base + wa + 32 * G::kWRow * j + wc0);
+      if constexpr (G::kMx)
+        sb[j] = *reinterpret_cast<const unsigned *>(base + G::kWS + (wr0 + 32 * j) * 4) >> shift;
+      else
+        fb[j][1] = *reinterpret_cast<const u32x4 *>(base + wa + 32 * G::kWRow * j + wc1);
+    }
+  };
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  const int last = steps - 1;
+  dma(0, 0);
+  dma(1, min(1, last));
+  sync();  // step 0 landed
+  read(0);
+  int cur = 0;
+  for (int t = 0; t < steps; ++t) {
+    const int nxt = cur == kStages - 1 ? 0 : cur + 1;
+    const int far = nxt == kStages - 1 ? 0 : nxt + 1;
+    // Stage `far` held step t - 1, whose fragments every wave read before the
+    // barrier of step t - 1.
+    dma(far, min(t + 2, last));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      i32x8 a;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) a[c] = static_cast<int>(fa[i][0][c]), a[4 + c] = static_cast<int>(fa[i][1][c]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        i32x8 b;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          b[c] = static_cast<int>(fb[j][0][c]);
+          b[4 + c] = G::kMx ? 0 : static_cast<int>(fb[j][1][c]);
+        }
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            a, b, acc[i][j], kFmtE4M3, G::kMx ? kFmtE2M1 : kFmtE4M3, 0, static_cast<int>(sa[i]), 0,
+            G::kMx ? static_cast<int>(sb[j]) : 127);
+      }
+    }
+    sync();  // step t + 1 landed; every wave's reads of step t are done
+    read(nxt);
+    cur = nxt;
+  }
+
+  // Partial sums of the two k-slices: group 1 stores, group 0 adds and writes.
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  float *exchange = reinterpret_cast<float *>(lds);
+  if (g == 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) exchange[((p * 8 + i * 2 + j) * 16 + v) * L2C_WAVE + lane] = acc[i][j][v];
+  }
+  __syncthreads();
+  if (g == 0) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = wn * 64 + 32 * j + r;
+      float rscale = 1.0f;
+      if constexpr (!G::kMx) rscale = n < nrows ? static_cast<const float *>(wscales)[n0 + n] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int m = wm * 128 + 32 * i + 8 * (v / 4) + 4 * h + v % 4;
+          const float sum = acc[i][j][v] + exchange[((p * 8 + i * 2 + j) * 16 + v) * L2C_WAVE + lane];
+          if (m < mrows && n < nrows) out[static_cast<size_t>(m0 + m) * N + n0 + n] = sum * rscale;
+        }
+    }
+  }
+}
+
+// Workspace views.
+struct Mxfp8View {
+  uint8_t *codes;
+  uint8_t *scales;
+};
+Mxfp8View view(void *workspace, int batch, int cols) {
+  uint8_t *w = static_cast<uint8_t *>(workspace);
+  return {w, w + round256(static_cast<size_t>(batch) * cols)};
+}
+
+// Argument checks shared by the entry points: 0 when the shape is accepted.
+int check_shape(int batch, int cols, int rows) {
+  if (batch < 0 || cols <= 0 || rows < 0 || cols % kBK != 0) return hipErrorInvalidValue;
+  // Per-lane byte offsets are computed in int: a tile's X rows, the W rows of
+  // a tile and the whole X scale array stay below 2^31.
+  if (static_cast<long long>(kBM) * cols > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (static_cast<long long>(padded4(batch)) * (cols / 32) > 0x7fffffffLL) return hipErrorInvalidValue;
+  return hipSuccess;
+}
+
+int launch_quantizer(const Mxfp8View &v, const uint16_t *X, int batch, int cols, hipStream_t stream) {
+  const long long lanes = static_cast<long long>(padded4(batch)) * (cols / 8);
+  const long long grid = (lanes + 255) / 256;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(quantize_mxfp8_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream, v.codes,
+                     v.scales, X, batch, padded4(batch), cols);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" size_t l2c_mxfp8_workspace_bytes(int batch, int cols) {
+  if (batch <= 0 || cols <= 0 || cols % kBK != 0) return 0;
+  return round256(static_cast<size_t>(batch) * cols) + static_cast<size_t>(cols / kBK) * padded4(batch) * 4;
+}
+
+extern "C" int l2c_quantize_mxfp8(void *workspace, size_t workspace_bytes, const uint16_t *Xbf16, int batch,
+                                  int cols, hipStream_t stream) {
+  if (const int e = check_shape(batch, cols, 0)) return e;
+  if (batch == 0) return hipSuccess;
+  if (!workspace || !Xbf16 || !l2c_aligned16(Xbf16) || !l2c_aligned16(workspace)) return hipErrorInvalidValue;
+  if (workspace_bytes < l2c_mxfp8_workspace_bytes(batch, cols)) return hipErrorInvalidValue;
+  return launch_quantizer(view(workspace, batch, cols), Xbf16, batch, cols, stream);
+}
+
+extern "C" int l2c_matmul_qs(float *out, const void *Xbf16, const void *Wq, const void *scales, int fmt, int batch,
+                             int cols, int rows, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (fmt != L2C_Q_MXFP4 && fmt != L2C_Q_FP8) return hipErrorInvalidValue;
+  if (const int e = check_shape(batch, cols, rows)) return e;
+  if (batch == 0 || rows == 0) return hipSuccess;
+  if (!out || !Xbf16 || !Wq || !scales || !workspace) return hipErrorInvalidValue;
+  if (!l2c_aligned16(Xbf16) || !l2c_aligned16(Wq) || !l2c_aligned16(workspace) ||
+      (reinterpret_cast<uintptr_t>(scales) & 3u))
+    return hipErrorInvalidValue;
+  if (workspace_bytes < l2c_mxfp8_workspace_bytes(batch, cols)) return hipErrorInvalidValue;
+  if (static_cast<long long>(kBN) * (fmt == L2C_Q_MXFP4 ? cols / 2 : cols) > 0x7fffffffLL) return hipErrorInvalidValue;
+  const long long tiles = static_cast<long long>((batch + kBM - 1) / kBM) * ((rows + kBN - 1) / kBN);
+  if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+  const Mxfp8View v = view(workspace, batch, cols);
+  if (const int e = launch_quantizer(v, static_cast<const uint16_t *>(Xbf16), batch, cols, stream)) return e;
+  const uint8_t *W = static_cast<const uint8_t *>(Wq);
+  if (fmt == L2C_Q_MXFP4)
+    hipLaunchKernelGGL(scaled_gemm_kernel<L2C_Q_MXFP4>, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream,
+                       out, v.codes, v.scales, W, scales, batch, rows, cols);
+  else
+    hipLaunchKernelGGL(scaled_gemm_kernel<L2C_Q_FP8>, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream,
+                       out, v.codes, v.scales, W, scales, batch, rows, cols);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+int l2c_scgemm_occupancy(int fmt, int *blocks_per_cu) {
+  const void *fn = fmt == L2C_Q_MXFP4 ? reinterpret_cast<const void *>(scaled_gemm_kernel<L2C_Q_MXFP4>)
+                                      : reinterpret_cast<const void *>(scaled_gemm_kernel<L2C_Q_FP8>);
+  return static_cast<int>(hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, kThreads, 0));
+}

@@ -23,6 +23,8 @@ const char *matmul_name(Matmul m) {
     case Matmul::kBatched: return "batched";
     case Matmul::kMxfp4: return "mxfp4";
     case Matmul::kFp8: return "fp8";
+    case Matmul::kMxfp4s: return "mxfp4s";
+    case Matmul::kFp8s: return "fp8s";
   }
   return "?";
 }
@@ -56,7 +58,7 @@ std::string usage_text(const char *program) {
   text += program;
   text +=
       " [graph|direct] [launches|auto] [batch] [size] [rows] [repeats] [warmup_ms]"
-      " [copy|nocopy] [naive|coalesced|fused|batched|mxfp4|fp8]"
+      " [copy|nocopy] [naive|coalesced|fused|batched|mxfp4|fp8|mxfp4s|fp8s]"
       " [deterministic|random[=SEED]|scaled[=SEED]|normal[=SEED]] [fullcheck] [warmup_iters=N]"
       " [--dump=FILE]\n";
   return text;
@@ -131,6 +133,7 @@ bool parse_options(int argc, const char *const *argv, Options *options, std::str
         {"naive", 4, Matmul::kNaive},         {"coalesced", 4, Matmul::kCoalesced},
         {"fused", 4, Matmul::kFused},         {"batched", 4, Matmul::kBatched},
         {"mxfp4", 4, Matmul::kMxfp4},         {"fp8", 4, Matmul::kFp8},
+        {"mxfp4s", 4, Matmul::kMxfp4s},       {"fp8s", 4, Matmul::kFp8s},
         {"fullcheck", 5, Matmul::kNaive}};
     bool matched = false;
     for (const Word &w : words) {
@@ -303,13 +306,16 @@ float e4m3_value(unsigned code) {
 }
 
 unsigned e4m3_encode(float v) {
-  static double mags[127];
-  static bool built = false;
-  if (!built) {
-    for (unsigned c = 0; c < 127; ++c) mags[c] = e4m3_value(c);
-    built = true;
-  }
-  const unsigned code = nearest_code(mags, 127, std::fabs(static_cast<double>(v)));
+  // A function-local static is initialized once, thread-safely: the encoder
+  // may be called from the validation's worker threads.
+  struct Table {
+    double mags[127];
+    Table() {
+      for (unsigned c = 0; c < 127; ++c) mags[c] = e4m3_value(c);
+    }
+  };
+  static const Table table;
+  const unsigned code = nearest_code(table.mags, 127, std::fabs(static_cast<double>(v)));
   return (code != 0 && v < 0) ? (code | 0x80u) : code;
 }
 
@@ -320,6 +326,16 @@ int mxfp4_block_exponent(float amax) {
   const int e = std::ilogb(amax);
   const double m = std::ldexp(static_cast<double>(amax), -e);
   const int x = m >= 1.5 ? e - 2 : e - 3;
+  return std::min(127, std::max(-127, x));
+}
+
+int mxfp8_block_exponent(float amax) {
+  if (!(amax > 0.0f)) return -127;
+  // Smallest X with amax <= 448 * 2^X = 1.75 * 2^(X + 8): with amax = m * 2^E,
+  // m in [1, 2), X = E - 8 when m <= 1.75 and E - 7 otherwise.
+  const int e = std::ilogb(amax);
+  const double m = std::ldexp(static_cast<double>(amax), -e);
+  const int x = m <= 1.75 ? e - 8 : e - 7;
   return std::min(127, std::max(-127, x));
 }
 

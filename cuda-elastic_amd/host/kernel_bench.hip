@@ -7,6 +7,9 @@
 //
 //   l2c_kernel_bench OP BATCH SIZE ROWS ITERS   (after >= 100 ms of warm-up launches)
 //   OP: rmsnorm softmax gemv naive fused matmul mxfp4 fp8 copy
+//       mxfp4s fp8s (the block-scaled product: MXFP8 activation quantizer +
+//       scaled contraction, as l2c_matmul_qs runs them; cvt_mxfp8 the
+//       quantizer alone)
 //       bf16 mxfp6 (lowprec classifier contractions, alpha on for bf16)
 //       cvt_bf16 cvt_mxfp6 cvt_nvfp4 (lowprec per-step activation conversions
 //       of BATCH x SIZE; cvt_nvfp4 = tensor scales + codes + bf16 expansion)
@@ -213,7 +216,8 @@ int main(int argc, char **argv) {
   CHECK(hipGetLastError());
 
   uint16_t *xb = nullptr, *wb = nullptr;
-  uint8_t *codes = nullptr, *sc8 = nullptr, *xq = nullptr, *xs = nullptr;
+  uint8_t *codes = nullptr, *sc8 = nullptr, *xq = nullptr, *xs = nullptr, *ws = nullptr;
+  size_t ws_bytes = 0;
   float *sc32 = nullptr, *alpha = nullptr, *partials = nullptr, *tscales = nullptr;
   if (op == "bf16" || op == "mxfp6" || op == "cvt_bf16" || op == "cvt_mxfp6" || op == "cvt_nvfp4") {
     if (S % 128 != 0) {
@@ -241,14 +245,23 @@ int main(int argc, char **argv) {
       L2C(l2c_quantize_mxfp6(codes, sc8, m, R, S, nullptr));
     }
   }
-  if (op == "mxfp4" || op == "fp8") {
+  const bool scaled = op == "mxfp4s" || op == "fp8s" || op == "cvt_mxfp8";
+  if (scaled) {
+    ws_bytes = l2c_mxfp8_workspace_bytes(B, S);
+    if (ws_bytes == 0) {
+      std::fprintf(stderr, "block-scaled ops need SIZE %% 128 == 0\n");
+      return 2;
+    }
+    CHECK(hipMalloc(&ws, ws_bytes));
+  }
+  if (op == "mxfp4" || op == "fp8" || scaled) {
     if (S % 32 != 0) {
       std::fprintf(stderr, "quantized ops need SIZE %% 32 == 0\n");
       return 2;
     }
     CHECK(hipMalloc(&xb, vec * 2));
     L2C(l2c_to_bf16(xb, x, vec, nullptr));
-    if (op == "mxfp4") {
+    if (op == "mxfp4" || op == "mxfp4s") {
       CHECK(hipMalloc(&codes, mat / 2));
       CHECK(hipMalloc(&sc8, mat / 32));
       L2C(l2c_quantize_mxfp4(codes, sc8, m, R, S, nullptr));
@@ -287,6 +300,15 @@ int main(int argc, char **argv) {
       bytes = vec * 2.0 + (op == "mxfp4" ? mat / 2.0 + mat / 32.0 : mat + R * 4.0) +
               static_cast<double>(B) * R * 4;
       flops = 2.0 * B * static_cast<double>(mat);
+    } else if (op == "mxfp4s" || op == "fp8s") {
+      const bool mx = op == "mxfp4s";
+      L2C(l2c_matmul_qs(prod, xb, codes, mx ? static_cast<const void *>(sc8) : sc32, mx ? L2C_Q_MXFP4 : L2C_Q_FP8, B,
+                        S, R, ws, ws_bytes, s));
+      bytes = vec * 2.0 + (mx ? mat / 2.0 + mat / 32.0 : mat + R * 4.0) + static_cast<double>(B) * R * 4;
+      flops = 2.0 * B * static_cast<double>(mat);
+    } else if (op == "cvt_mxfp8") {
+      L2C(l2c_quantize_mxfp8(ws, ws_bytes, xb, B, S, s));
+      bytes = vec * (2.0 + 1.0 + 1.0 / 32);
     } else if (op == "bf16") {
       L2C(l2c_matmul_bf16(prod, xb, wb, alpha, B, S, R, s));
       bytes = (vec + static_cast<double>(mat)) * 2 + static_cast<double>(B) * R * 4;

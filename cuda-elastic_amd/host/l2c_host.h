@@ -32,14 +32,19 @@ enum class Matmul : int32_t {
   kBatched = 3,    // out[b][r] = sum_k W[r][k] x[b][k] on fp32 MFMA
   kMxfp4 = 4,      // batched, bf16 activations x MXFP4 weights
   kFp8 = 5,        // batched, bf16 activations x per-row-scaled fp8 e4m3 weights
+  kMxfp4s = 6,     // mxfp4 weights on the block-scaled matrix cores, MXFP8 activations
+  kFp8s = 7,       // fp8 weights on the block-scaled matrix cores, MXFP8 activations
 };
 
 const char *matmul_name(Matmul m);
 const char *input_name(InputMode m);
-inline bool matmul_is_batched(Matmul m) {
-  return m == Matmul::kBatched || m == Matmul::kMxfp4 || m == Matmul::kFp8;
+inline bool matmul_is_scaled(Matmul m) { return m == Matmul::kMxfp4s || m == Matmul::kFp8s; }
+inline bool matmul_is_quantized(Matmul m) {
+  return m == Matmul::kMxfp4 || m == Matmul::kFp8 || matmul_is_scaled(m);
 }
-inline bool matmul_is_quantized(Matmul m) { return m == Matmul::kMxfp4 || m == Matmul::kFp8; }
+inline bool matmul_is_batched(Matmul m) { return m == Matmul::kBatched || matmul_is_quantized(m); }
+// MXFP4 weights (else per-row fp8) for a quantized variant.
+inline bool matmul_is_mxfp4(Matmul m) { return m == Matmul::kMxfp4 || m == Matmul::kMxfp4s; }
 
 struct InputOptions {
   InputMode mode = InputMode::kDeterministic;
@@ -105,6 +110,7 @@ unsigned e2m1_encode(double v);          // nearest, ties to even code, saturati
 float e4m3_value(unsigned code);         // OCP e4m3fn, bias 7
 unsigned e4m3_encode(float v);           // nearest even, saturating at 448
 int mxfp4_block_exponent(float amax);    // floor(log2(amax / 6)) clamped to [-127, 127]
+int mxfp8_block_exponent(float amax);    // ceil(log2(amax / 448)) clamped to [-127, 127]
 
 // ---------------------------------------------------------------------------
 // Validation (restates llama2c/llama2c_common.h:139-319 and extends it to
@@ -126,6 +132,9 @@ struct Validation {
   double softmax_max_abs_error = 0, softmax_max_rel_error = 0;
   double product_max_ratio = 0;     // max |p - ref| / tol
   double product_max_rel_error = 0; // max |p - ref| / max(|ref|, sum |terms| * 2^-24)
+  // Block-scaled variants only: max |p - ref_bf16| / sum |terms| against the
+  // bf16-activation reference (the error activation quantization adds).
+  double product_bf16_act_rel_error = 0;
   ProductCheck product;
 };
 
@@ -142,6 +151,9 @@ struct QuantOperands {
   std::vector<uint8_t> codes;     // mxfp4: rows x size/2; fp8: rows x size
   std::vector<uint8_t> scales_e8; // mxfp4: rows x size/32
   std::vector<float> scales_f32;  // fp8: rows
+  // Block-scaled variants: the device's MXFP8 activations, row-major codes
+  // [batch][size] and scale bytes [batch][size / 32].
+  std::vector<uint8_t> x_codes, x_scales;
 };
 
 Validation validate_all(const Options &options, const Inputs &inputs, const Outputs &outputs,

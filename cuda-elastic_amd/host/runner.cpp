@@ -137,10 +137,12 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
     const size_t mat_elems = static_cast<size_t>(R) * S;
     const size_t prod_elems = batched ? static_cast<size_t>(B) * R : static_cast<size_t>(R);
     if (quantized && S % 32 != 0) throw Failure{"mxfp4/fp8 variants need size % 32 == 0"};
+    const bool scaled = matmul_is_scaled(mm);
+    if (scaled && S % 128 != 0) throw Failure{"mxfp4s/fp8s variants need size % 128 == 0"};
 
     DeviceBuffer<float> d_input, d_weight, d_prob, d_softmax, d_matrix, d_normalized, d_product;
     DeviceBuffer<uint16_t> d_xbf16;
-    DeviceBuffer<uint8_t> d_codes, d_scales8;
+    DeviceBuffer<uint8_t> d_codes, d_scales8, d_workspace;
     DeviceBuffer<float> d_scales32;
     d_input.alloc(vec_elems);
     d_prob.alloc(vec_elems);
@@ -157,11 +159,14 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
     // Quantized variants: bf16 activations and quantized weights are prepared
     // once on the device (setup, untimed), then copied back for the oracle.
     const void *q_scales = nullptr;
-    const int qfmt = mm == Matmul::kMxfp4 ? L2C_Q_MXFP4 : L2C_Q_FP8;
+    const int qfmt = matmul_is_mxfp4(mm) ? L2C_Q_MXFP4 : L2C_Q_FP8;
     if (quantized) {
       d_xbf16.alloc(vec_elems);
+      // The block-scaled variants quantize the activations into this
+      // workspace on every iteration (inside l2c_matmul_qs).
+      if (scaled) d_workspace.alloc(l2c_mxfp8_workspace_bytes(B, S));
       L2C_OK(l2c_to_bf16(d_xbf16.ptr, d_input.ptr, vec_elems, nullptr));
-      if (mm == Matmul::kMxfp4) {
+      if (matmul_is_mxfp4(mm)) {
         d_codes.alloc(mat_elems / 2);
         d_scales8.alloc(mat_elems / 32);
         L2C_OK(l2c_quantize_mxfp4(d_codes.ptr, d_scales8.ptr, d_matrix.ptr, R, S, nullptr));
@@ -177,7 +182,7 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
       HIP_OK(hipMemcpy(quant->x_bf16.data(), d_xbf16.ptr, vec_elems * 2, hipMemcpyDeviceToHost));
       quant->codes.resize(d_codes.count);
       HIP_OK(hipMemcpy(quant->codes.data(), d_codes.ptr, d_codes.count, hipMemcpyDeviceToHost));
-      if (mm == Matmul::kMxfp4) {
+      if (matmul_is_mxfp4(mm)) {
         quant->scales_e8.resize(d_scales8.count);
         HIP_OK(hipMemcpy(quant->scales_e8.data(), d_scales8.ptr, d_scales8.count, hipMemcpyDeviceToHost));
       } else {
@@ -219,7 +224,7 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
       else if (mm == Matmul::kBatched)
         res->matmul_waves = waves(L2C_OP_MATMUL, 0);
       else
-        res->matmul_waves = waves(L2C_OP_MATMUL_Q, qfmt);
+        res->matmul_waves = waves(scaled ? L2C_OP_MATMUL_QS : L2C_OP_MATMUL_Q, qfmt);
     }
 
     // Algorithmic bytes and flops per launch of each operation.
@@ -231,7 +236,7 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
       res->matmul.flops = 2.0 * R * S;
     } else {
       const double wbytes = mm == Matmul::kBatched ? mat_elems * 4.0
-                            : mm == Matmul::kMxfp4 ? mat_elems / 2.0 + mat_elems / 32.0
+                            : matmul_is_mxfp4(mm) ? mat_elems / 2.0 + mat_elems / 32.0
                                                    : mat_elems * 1.0 + R * 4.0;
       const double xbytes = vec_elems * (quantized ? 2.0 : 4.0);
       res->matmul.bytes = xbytes + wbytes + static_cast<double>(B) * R * 4.0;
@@ -260,6 +265,11 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
         case Matmul::kMxfp4:
         case Matmul::kFp8:
           L2C_OK(l2c_matmul_q(d_product.ptr, d_xbf16.ptr, d_codes.ptr, q_scales, qfmt, B, S, R, s));
+          break;
+        case Matmul::kMxfp4s:
+        case Matmul::kFp8s:
+          L2C_OK(l2c_matmul_qs(d_product.ptr, d_xbf16.ptr, d_codes.ptr, q_scales, qfmt, B, S, R,
+                               d_workspace.ptr, d_workspace.count, s));
           break;
         case Matmul::kFused:
           break;
@@ -416,6 +426,19 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
       d2h(h_product.ptr, d_product.ptr, prod_elems, st.mm);
       synchronize_all();
     }
+    // The MXFP8 activations the block-scaled product used (the workspace
+    // layout of include/l2c.h: row-major codes, then [S/128][Bp][4] scales).
+    if (scaled) {
+      quant->x_codes.resize(vec_elems);
+      HIP_OK(hipMemcpy(quant->x_codes.data(), d_workspace.ptr, vec_elems, hipMemcpyDeviceToHost));
+      const size_t off = (vec_elems + 255) / 256 * 256, bp = (static_cast<size_t>(B) + 3) / 4 * 4;
+      std::vector<uint8_t> tiles(static_cast<size_t>(S / 128) * bp * 4);
+      HIP_OK(hipMemcpy(tiles.data(), d_workspace.ptr + off, tiles.size(), hipMemcpyDeviceToHost));
+      quant->x_scales.resize(vec_elems / 32);
+      for (size_t b = 0; b < static_cast<size_t>(B); ++b)
+        for (size_t j = 0; j < static_cast<size_t>(S / 32); ++j)
+          quant->x_scales[b * (S / 32) + j] = tiles[((j / 4) * bp + b) * 4 + j % 4];
+    }
     normalized->assign(h_normalized.ptr, h_normalized.ptr + vec_elems);
     softmax->assign(h_softmax.ptr, h_softmax.ptr + vec_elems);
     product->assign(h_product.ptr, h_product.ptr + prod_elems);
@@ -472,12 +495,15 @@ std::string result_line(const Options &o, const RunResult &r, const Validation &
   constexpr double kHbmPeakGbps = 8000.0;         // MI355X HBM3E
   constexpr double kFp32MfmaPeakTflops = 157.3;   // dense fp32 matrix
   constexpr double kBf16MfmaPeakTflops = 2500.0;  // dense bf16 matrix
+  constexpr double kFp8MfmaPeakTflops = 5000.0;   // dense fp8 matrix (the block-scaled products)
   const double gpu_ms_per_iter = r.gpu_ms / r.launches;
   const double achieved_gbps = r.min_bytes_per_iter / (gpu_ms_per_iter * 1.0e6);
   auto gbps = [](const KernelTiming &t) { return t.us > 0 ? t.bytes / (t.us * 1.0e3) : 0.0; };
   const bool batched = matmul_is_batched(o.matmul);
   const double mm_tflops = r.matmul.us > 0 ? r.matmul.flops / (r.matmul.us * 1.0e6) : 0.0;
-  const double mm_peak = o.matmul == Matmul::kBatched ? kFp32MfmaPeakTflops : kBf16MfmaPeakTflops;
+  const double mm_peak = o.matmul == Matmul::kBatched   ? kFp32MfmaPeakTflops
+                         : matmul_is_scaled(o.matmul) ? kFp8MfmaPeakTflops
+                                                      : kBf16MfmaPeakTflops;
   const double mm_frac = batched ? mm_tflops / mm_peak : gbps(r.matmul) / kHbmPeakGbps;
   const double strict_product = matmul_is_quantized(o.matmul) ? 2.0e-3 : 1.0e-4 * std::sqrt(static_cast<double>(o.size));
   const bool strict_valid = v.valid && v.rms_max_rel_error <= 1.0e-5 && v.softmax_max_rel_error <= 1.0e-5 &&
@@ -496,7 +522,7 @@ std::string result_line(const Options &o, const RunResult &r, const Validation &
       "softmax_gbps=%.1f softmax_hbm_frac=%.4f matmul_us=%.3f matmul_gbps=%.1f matmul_tflops=%.3f "
       "matmul_bound=%s matmul_frac=%.4f rms_max_rel_err=%.3e softmax_max_rel_err=%.3e "
       "product_max_rel_err=%.3e product_max_tol_ratio=%.3e check_vectors=%zu strict_valid=%d "
-      "matmul_within_iter=%d",
+      "matmul_within_iter=%d product_bf16_act_rel_err=%.3e",
       o.graph ? "graph" : "direct", matmul_name(o.matmul), r.launches, o.batch, o.size, o.rows,
       o.repeats, o.copy_outputs ? 1 : 0, o.warmup_ms, r.warmup_iterations, r.gpu_ms, gpu_ms_per_iter,
       kSingleIterations, r.single_us, r.wall_ms, r.wall_ms / r.launches, r.submit_us,
@@ -511,7 +537,7 @@ std::string result_line(const Options &o, const RunResult &r, const Validation &
       batched ? "mfma" : "hbm", mm_frac, v.rms_max_rel_error, v.softmax_max_rel_error,
       v.product_max_rel_error, v.product_max_ratio,
       batched ? v.product.sampled_batch_rows.size() : static_cast<size_t>(1), strict_valid ? 1 : 0,
-      r.matmul.us <= gpu_ms_per_iter * 1000.0 ? 1 : 0);
+      r.matmul.us <= gpu_ms_per_iter * 1000.0 ? 1 : 0, v.product_bf16_act_rel_error);
   std::string line = buf;
   // Device names may contain spaces; keep the line space-separated key=value.
   const size_t d = line.find(" device=");

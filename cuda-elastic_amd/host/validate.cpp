@@ -27,9 +27,10 @@ namespace {
 
 struct Acc {
   bool valid = true;
-  double rms_abs = 0, rms_rel = 0, sm_abs = 0, sm_rel = 0, ratio = 0, prel = 0;
+  double rms_abs = 0, rms_rel = 0, sm_abs = 0, sm_rel = 0, ratio = 0, prel = 0, bf16 = 0;
   void merge(const Acc &o) {
     valid = valid && o.valid;
+    bf16 = std::max(bf16, o.bf16);
     rms_abs = std::max(rms_abs, o.rms_abs);
     rms_rel = std::max(rms_rel, o.rms_rel);
     sm_abs = std::max(sm_abs, o.sm_abs);
@@ -108,7 +109,7 @@ void check_vector_deterministic(const Inputs &in, const Outputs &out, int size, 
 // matmul" uses it).
 void dequant_row(const Options &o, const QuantOperands &q, int r, float *w) {
   const int size = o.size;
-  if (o.matmul == Matmul::kMxfp4) {
+  if (matmul_is_mxfp4(o.matmul)) {
     const uint8_t *codes = q.codes.data() + static_cast<size_t>(r) * (size / 2);
     const uint8_t *sc = q.scales_e8.data() + static_cast<size_t>(r) * (size / 32);
     for (int k = 0; k < size; ++k) {
@@ -173,13 +174,27 @@ Validation validate_all(const Options &o, const Inputs &in, const Outputs &out,
   pc.tolerance.assign(out_elems, batched ? std::numeric_limits<float>::quiet_NaN() : 0.0f);
   pc.reference.assign(out_elems, batched ? std::numeric_limits<double>::quiet_NaN() : 0.0);
 
-  // Activations as the product saw them (bf16-rounded for quantized variants).
-  std::vector<float> xq;
+  // Activations as the product saw them (bf16-rounded for quantized variants;
+  // for the block-scaled ones, the device's MXFP8 codes times their block
+  // scales, exact in float).
+  std::vector<float> xq, x16;
+  const bool scaled = matmul_is_scaled(o.matmul);
   if (quantized) {
     xq.resize(static_cast<size_t>(batch) * size);
     for (size_t i = 0; i < xq.size(); ++i) xq[i] = bf16_value(quant->x_bf16[i]);
   }
+  if (scaled) {
+    x16.swap(xq);
+    xq.resize(x16.size());
+    for (size_t i = 0; i < xq.size(); ++i)
+      xq[i] = std::ldexp(e4m3_value(quant->x_codes[i]), static_cast<int>(quant->x_scales[i / 32]) - 127);
+  }
   const float *xs = quantized ? xq.data() : in.input.data();
+  // The block-scaled products take the implementation-check bound of a
+  // block-scaled GEMM, experiments/blackwell/lowprec/spec.json:55-62:
+  // gamma_K sum |terms| + u |reference| with u = 2^-23.
+  const double u23 = std::ldexp(1.0, -23);
+  const double gamma_k = static_cast<double>(size) * u23 / (1.0 - static_cast<double>(size) * u23);
 
   parallel_ranges(static_cast<size_t>(rows), threads, [&](size_t r0, size_t r1, size_t) {
     Acc acc;
@@ -198,7 +213,20 @@ Validation validate_all(const Options &o, const Inputs &in, const Outputs &out,
           sum += term;
           magnitude += std::fabs(term);
         }
-        const double tolerance = gamma * magnitude + FLT_MIN;
+        double tolerance = gamma * magnitude + FLT_MIN;
+        if (scaled) {
+          tolerance = gamma_k * magnitude + u23 * std::fabs(sum) + FLT_MIN;
+          // Against the bf16 activations (reported, not a validity condition).
+          const float *x2 = x16.data() + static_cast<size_t>(b) * size;
+          double s16 = 0.0, m16 = 0.0;
+          for (int c = 0; c < size; ++c) {
+            const double term = static_cast<double>(m[c]) * x2[c];
+            s16 += term;
+            m16 += std::fabs(term);
+          }
+          const double got16 = out.product[static_cast<size_t>(b) * rows + r];
+          acc.bf16 = std::max(acc.bf16, err_or_inf(std::fabs(got16 - s16)) / (m16 > 0 ? m16 : 1.0));
+        }
         const size_t at = batched ? static_cast<size_t>(b) * rows + r : r;
         pc.tolerance[at] = static_cast<float>(tolerance);
         pc.reference[at] = sum;
@@ -226,6 +254,7 @@ Validation validate_all(const Options &o, const Inputs &in, const Outputs &out,
   v.softmax_max_rel_error = total.sm_rel;
   v.product_max_ratio = total.ratio;
   v.product_max_rel_error = total.prel;
+  v.product_bf16_act_rel_error = total.bf16;
   return v;
 }
 

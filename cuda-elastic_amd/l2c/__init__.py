@@ -35,7 +35,7 @@ MATVEC_NAIVE = 0
 MATVEC_COALESCED = 1
 Q_MXFP4 = 0
 Q_FP8 = 1
-OP_RMSNORM, OP_SOFTMAX, OP_MATVEC, OP_FUSED, OP_MATMUL, OP_MATMUL_Q = range(6)
+OP_RMSNORM, OP_SOFTMAX, OP_MATVEC, OP_FUSED, OP_MATMUL, OP_MATMUL_Q, OP_MATMUL_QS = range(7)
 
 # Symbols declared in include/l2c.h and include/l2c_harness.h.
 KERNEL_SYMBOLS = (
@@ -45,6 +45,7 @@ KERNEL_SYMBOLS = (
     "l2c_decoder_init_model", "l2c_decoder_rmsnorm", "l2c_decoder_softmax_argmax",
     "l2c_quantize_mxfp6", "l2c_nvfp4_tensor_scales", "l2c_quantize_nvfp4", "l2c_to_bf16_x4",
     "l2c_matmul_bf16", "l2c_matmul_mxfp6", "l2c_mxfp6_bytes",
+    "l2c_matmul_qs", "l2c_quantize_mxfp8", "l2c_mxfp8_workspace_bytes",
 )
 NVFP4_PARTIALS = 1024  # L2C_NVFP4_PARTIALS
 HOST_SYMBOLS = ("l2c_harness_main", "l2c_compare_dumps", "l2c_decoder_main", "l2c_decoder_run",
@@ -103,11 +104,15 @@ def load() -> ctypes.CDLL:
         "l2c_to_bf16_x4": [p, p, ctypes.c_longlong, p],
         "l2c_matmul_bf16": [p, p, p, p, i, i, i, p],
         "l2c_matmul_mxfp6": [p, p, p, p, p, i, i, i, p],
+        "l2c_matmul_qs": [p, p, p, p, i, i, i, i, p, sz, p],
+        "l2c_quantize_mxfp8": [p, sz, p, i, i, p],
     }
     for name, args in sigs.items():
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = ctypes.c_int
+    lib.l2c_mxfp8_workspace_bytes.argtypes = [i, i]
+    lib.l2c_mxfp8_workspace_bytes.restype = sz
     lib.l2c_mxfp6_bytes.argtypes = [i, i, ctypes.POINTER(sz), ctypes.POINTER(sz)]
     lib.l2c_mxfp6_bytes.restype = ctypes.c_int
     lib.l2c_strerror.argtypes = [ctypes.c_int]
@@ -208,6 +213,30 @@ def matmul(out, X, W, batch, cols, rows, stream=None):
 def matmul_q(out, xbf16, wq, scales, fmt, batch, cols, rows, stream=None):
     _check(load().l2c_matmul_q(_vp(_ptr(out)), _vp(_ptr(xbf16)), _vp(_ptr(wq)), _vp(_ptr(scales)),
                                fmt, batch, cols, rows, _vp(_stream(stream))), "l2c_matmul_q")
+
+
+def mxfp8_workspace_bytes(batch, cols):
+    return load().l2c_mxfp8_workspace_bytes(batch, cols)
+
+
+def mxfp8_views(workspace, batch, cols):
+    """(codes [batch*cols], scales [cols/128][Bp][4]) views of an l2c_matmul_qs
+    workspace (uint8 tensor), as include/l2c.h lays it out."""
+    n = batch * cols
+    off = (n + 255) // 256 * 256
+    bp = (batch + 3) // 4 * 4
+    return workspace[:n], workspace[off:off + (cols // 128) * bp * 4]
+
+
+def matmul_qs(out, xbf16, wq, scales, fmt, batch, cols, rows, workspace, stream=None):
+    _check(load().l2c_matmul_qs(_vp(_ptr(out)), _vp(_ptr(xbf16)), _vp(_ptr(wq)), _vp(_ptr(scales)), fmt, batch,
+                                cols, rows, _vp(_ptr(workspace)), workspace.numel() * workspace.element_size(),
+                                _vp(_stream(stream))), "l2c_matmul_qs")
+
+
+def quantize_mxfp8(workspace, xbf16, batch, cols, stream=None):
+    _check(load().l2c_quantize_mxfp8(_vp(_ptr(workspace)), workspace.numel() * workspace.element_size(),
+                                     _vp(_ptr(xbf16)), batch, cols, _vp(_stream(stream))), "l2c_quantize_mxfp8")
 
 
 def quantize_mxfp4(codes, scales, W, rows, cols, stream=None):

@@ -26,6 +26,9 @@
  *   l2c_matmul_q  no kernel in the reference: the quantized-weight matmul of the
  *                 benchmark configuration (MXFP4 / per-row fp8 weights, bf16
  *                 activations); its codes follow experiments/blackwell/lowprec/reference.cpp:13-96
+ *   l2c_matmul_qs the same product on the block-scaled matrix cores, activations
+ *                 quantized to MXFP8: the analogue of the reference's block-scaled
+ *                 CUTLASS GEMM, experiments/blackwell/lowprec/decoder_lowprec.cu:95-121
  *   l2c_decoder_init_model      init_model_kernel      applications/loom_private/decoder/decoder.cu:27-43
  *   l2c_decoder_rmsnorm         rmsnorm_kernel         applications/loom_private/decoder/decoder.cu:45-77
  *   l2c_decoder_softmax_argmax  softmax_argmax_kernel  applications/loom_private/decoder/decoder.cu:127-198
@@ -112,6 +115,36 @@ int l2c_matmul(float *out, const float *X, const float *W, int batch, int cols, 
  */
 int l2c_matmul_q(float *out, const void *Xbf16, const void *Wq, const void *scales, int fmt,
                  int batch, int cols, int rows, hipStream_t stream);
+
+/*
+ * Block-scaled quantized-weight contraction (the quantized-weight path on the
+ * gfx950 scaled matrix cores, v_mfma_scale_f32_32x32x64_f8f6f4):
+ *   out[b][r] = sum_k deq(MXFP8(Xbf16))[b][k] * deq(Wq, scales)[r][k]
+ * Wq / scales / fmt are exactly l2c_matmul_q's weight operand. The activations
+ * are first quantized on the device to MXFP8 into `workspace`: per 32
+ * consecutive k one UE8M0 scale 2^X with X the smallest exponent for which
+ * block max <= 448 * 2^X (ceil(log2(block max / 448)), clamped to
+ * [-127, 127]; a zero block gets X = -127), elements e4m3(x * 2^-X)
+ * nearest-even (the MX layout of experiments/blackwell/lowprec/spec.json
+ * "mxfp6", with a scale that never clips the block maximum). The products of
+ * the dequantized operands are exact; accumulation is FP32; the fp8 weights'
+ * row scale multiplies each output.
+ * Needs cols % 128 == 0; Xbf16, Wq and workspace 16-byte aligned, scales
+ * 4-byte aligned; workspace_bytes >= l2c_mxfp8_workspace_bytes(batch, cols).
+ *
+ * Workspace layout (what l2c_quantize_mxfp8 writes): e4m3 codes row-major
+ * [batch][cols] at offset 0; at offset round_up(batch * cols, 256) the scale
+ * bytes in k-step tiles [cols / 128][Bp][4], Bp = batch rounded up to a
+ * multiple of 4, byte j of a row's 4 = block j of that 128-k step, rows past
+ * batch zero. l2c_mxfp8_workspace_bytes returns 0 for an unsupported shape.
+ * Calls that share a workspace must be ordered on one stream.
+ */
+int l2c_matmul_qs(float *out, const void *Xbf16, const void *Wq, const void *scales, int fmt,
+                  int batch, int cols, int rows, void *workspace, size_t workspace_bytes,
+                  hipStream_t stream);
+int l2c_quantize_mxfp8(void *workspace, size_t workspace_bytes, const uint16_t *Xbf16, int batch,
+                       int cols, hipStream_t stream);
+size_t l2c_mxfp8_workspace_bytes(int batch, int cols);
 
 /*
  * Quantizers for l2c_matmul_q's weight operand, run on the device (setup work,
@@ -219,7 +252,8 @@ enum l2c_op {
   L2C_OP_MATVEC = 2,
   L2C_OP_FUSED = 3,
   L2C_OP_MATMUL = 4,
-  L2C_OP_MATMUL_Q = 5
+  L2C_OP_MATMUL_Q = 5,
+  L2C_OP_MATMUL_QS = 6  /* the contraction kernel of l2c_matmul_qs */
 };
 
 /*

@@ -18,6 +18,17 @@
  *   orc_e2m1_encode, orc_ue4m3_encode, orc_bf16 : against oracle/_ref
  *                                   (lowprec encode / to_bf16), exhaustively
  *   orc_mxfp4_exponent            : closed form 6 * 2^X <= amax < 6 * 2^(X+1)
+ *   orc_quantize_mxfp4_row,
+ *   orc_quantize_fp8_row,
+ *   orc_qmatmul_ref               : exact round trips of representable blocks
+ *                                   and rows, saturation and nearest-value
+ *                                   properties, an integer-exact dot product
+ *                                   (tests/test_golden.py)
+ *   orc_mxfp8_exponent,
+ *   orc_quantize_mxfp8_row,
+ *   orc_qsmatmul_ref              : the same kinds of closed forms, and equality
+ *                                   with orc_qmatmul_ref on activations MXFP8
+ *                                   represents exactly
  *   orc_iteration_f32             : llama2.c loop order; pinned against the
  *                                   double references within fp32 bounds
  *   orc_iteration_f32_mt          : the same loops split over OpenMP threads
@@ -553,6 +564,97 @@ void orc_quantize_fp8(const float *W, int rows, int cols, uint8_t *codes, float 
   int r;
   for (r = 0; r < rows; ++r)
     scales[r] = orc_quantize_fp8_row(W + (size_t)r * cols, cols, codes + (size_t)r * cols);
+}
+
+/* ------------------------------------------------------------------------ */
+/* MXFP8 activations of the block-scaled quantized contraction: E4M3 codes    */
+/* with one UE8M0 scale 2^X per 32 values, X the smallest exponent for which  */
+/* the block fits E4M3's range, X = ceil(log2(block max / 448)) clamped to    */
+/* [-127, 127]; elements nearest-even (saturation never triggers). This is    */
+/* the MX layout of experiments/blackwell/lowprec/spec.json "mxfp6" with a    */
+/* scale that does not clip the block maximum (spec.json's floor(log2 amax) - */
+/* emax would map maxima into [448, 512) * 2^X onto 448). No reference kernel */
+/* uses MXFP8; the recipe is pinned by closed forms in tests/test_golden.py.  */
+
+/* Smallest X with amax <= 448 * 2^X, clamped to [-127, 127]; -127 for
+ * amax = 0. Found by stepping X, exact in double. */
+int orc_mxfp8_exponent(float amax) {
+  int x = -127;
+  if (!(amax > 0.0f)) return -127;
+  while (x < 127 && ldexp(448.0, x) < (double)amax) ++x;
+  return x;
+}
+
+static float bf16_to_float(uint16_t b) {
+  const uint32_t bits = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+/* One row of bf16 activations: e4m3 codes (one byte each) and one UE8M0
+ * scale byte per 32 values. */
+void orc_quantize_mxfp8_row(const uint16_t *xbf16, int cols, uint8_t *codes, uint8_t *scales) {
+  int blk, i;
+  for (blk = 0; blk * 32 < cols; ++blk) {
+    float amax = 0.0f;
+    int x;
+    for (i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(bf16_to_float(xbf16[blk * 32 + i])));
+    x = orc_mxfp8_exponent(amax);
+    scales[blk] = (uint8_t)(x + 127);
+    for (i = 0; i < 32; ++i)
+      codes[blk * 32 + i] = (uint8_t)orc_ue4m3_encode(ldexp((double)bf16_to_float(xbf16[blk * 32 + i]), -x));
+  }
+}
+
+/* Row-major codes [rows][cols] and scales [rows][cols / 32]. */
+void orc_quantize_mxfp8(const uint16_t *X, int rows, int cols, uint8_t *codes, uint8_t *scales) {
+  int r;
+  for (r = 0; r < rows; ++r)
+    orc_quantize_mxfp8_row(X + (size_t)r * cols, cols, codes + (size_t)r * cols, scales + (size_t)r * (cols / 32));
+}
+
+static double e4m3_signed_value(unsigned c) {
+  const double v = orc_ue4m3_value(c & 0x7fu);
+  return (c & 0x80u) ? -v : v;
+}
+
+/* Reference of the block-scaled contraction for the listed vectors: both
+ * operands dequantized exactly (MXFP8 activations; MXFP4 weights, or e4m3
+ * weights times their fp32 row scale) and accumulated in double, the
+ * arithmetic the implementation check of experiments/blackwell/lowprec/
+ * spec.json:55-62 compares a block-scaled GEMM with. xcodes / xscales are
+ * row-major [batch][size] / [batch][size / 32]; out is [b * rows + r]; mag
+ * receives sum |terms|. */
+void orc_qsmatmul_ref(int fmt, const uint8_t *xcodes, const uint8_t *xscales, const uint8_t *wcodes,
+                      const void *wscales, int size, int rows, const int *vectors, int nvectors, double *out,
+                      double *mag) {
+  int v, r, k;
+  double *w = (double *)malloc((size_t)size * sizeof(double));
+  double *a = (double *)malloc((size_t)size * sizeof(double));
+  for (v = 0; v < nvectors; ++v) {
+    const int b = vectors[v];
+    for (k = 0; k < size; ++k)
+      a[k] = ldexp(e4m3_signed_value(xcodes[(size_t)b * size + k]), (int)xscales[(size_t)b * (size / 32) + k / 32] - 127);
+    for (r = 0; r < rows; ++r) {
+      double s = 0.0, m = 0.0;
+      for (k = 0; k < size; ++k) {
+        if (fmt == 0) {
+          const uint8_t byte = wcodes[(size_t)r * (size / 2) + k / 2];
+          const uint8_t sc = ((const uint8_t *)wscales)[(size_t)r * (size / 32) + k / 32];
+          w[k] = ldexp(orc_e2m1_value((byte >> (4 * (k % 2))) & 15u), (int)sc - 127);
+        } else {
+          w[k] = e4m3_signed_value(wcodes[(size_t)r * size + k]) * (double)((const float *)wscales)[r];
+        }
+        s += a[k] * w[k];
+        m += fabs(a[k] * w[k]);
+      }
+      out[(size_t)b * rows + r] = s;
+      if (mag) mag[(size_t)b * rows + r] = m;
+    }
+  }
+  free(w);
+  free(a);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -66,6 +66,9 @@ def lib():
     L.orc_quantize_mxfp4.argtypes = [_f32p, i, i, _u8p, _u8p]
     L.orc_quantize_fp8.argtypes = [_f32p, i, i, _u8p, _f32p]
     L.orc_qmatmul_ref.argtypes = [i, _u16p, _u8p, _c.c_void_p, i, i, _i32p, i, _f64p, _f64p]
+    L.orc_mxfp8_exponent.argtypes, L.orc_mxfp8_exponent.restype = [f], i
+    L.orc_quantize_mxfp8.argtypes = [_u16p, i, i, _u8p, _u8p]
+    L.orc_qsmatmul_ref.argtypes = [i, _u8p, _u8p, _u8p, _c.c_void_p, i, i, _i32p, i, _f64p, _f64p]
     L.orc_e3m2_value.argtypes, L.orc_e3m2_value.restype = [_c.c_uint], d
     L.orc_e3m2_encode_array.argtypes = [_f64p, sz, _u8p]
     L.orc_mxfp6_exponent.argtypes, L.orc_mxfp6_exponent.restype = [f], i
@@ -303,6 +306,28 @@ def qmatmul_ref(fmt, xbf16, codes_packed, scales, size, rows, vectors, batch):
     lib().orc_qmatmul_ref(fmt, np.ascontiguousarray(xbf16, np.uint16),
                           np.ascontiguousarray(codes_packed, np.uint8),
                           scales.ctypes.data_as(ctypes.c_void_p), size, rows, vec, len(vec), out, mag)
+    return out, mag
+
+
+def quantize_mxfp8(xbf16, rows, cols):
+    """bf16 activations (uint16) to row-major e4m3 codes [rows*cols] and
+    UE8M0 scale codes [rows*cols/32]."""
+    codes = np.empty(rows * cols, np.uint8)
+    scales = np.empty(rows * cols // 32, np.uint8)
+    lib().orc_quantize_mxfp8(np.ascontiguousarray(xbf16, np.uint16), rows, cols, codes, scales)
+    return codes, scales
+
+
+def qsmatmul_ref(fmt, xcodes, xscales, wcodes_packed, wscales, size, rows, vectors, batch):
+    """Both operands dequantized, double accumulation: (out, sum |terms|),
+    each [batch * rows], NaN outside the listed vectors."""
+    vec = np.ascontiguousarray(vectors, np.int32)
+    out = np.full(batch * rows, np.nan, np.float64)
+    mag = np.full(batch * rows, np.nan, np.float64)
+    wscales = np.ascontiguousarray(wscales)
+    lib().orc_qsmatmul_ref(fmt, np.ascontiguousarray(xcodes, np.uint8), np.ascontiguousarray(xscales, np.uint8),
+                           np.ascontiguousarray(wcodes_packed, np.uint8), wscales.ctypes.data_as(ctypes.c_void_p),
+                           size, rows, vec, len(vec), out, mag)
     return out, mag
 
 

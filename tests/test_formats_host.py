@@ -108,3 +108,18 @@ def test_row_quantizers(F, orc):
         # The expansion is exact in bf16.
         assert not (ex.view(np.uint32) & 0xFFFF).any()
     assert F.l2cf_nvfp4_encode_scale(0.0) == 1.0
+
+
+def test_host_mxfp8_exponent_matches_oracle(orc):
+    """The harness's host MXFP8 block exponent (the closed form on the
+    significand) equals the oracle's stepping definition."""
+    import ctypes
+    import l2c
+    host = ctypes.CDLL(l2c.HOST_LIB_PATH)
+    fn = host._ZN8l2c_host20mxfp8_block_exponentEf
+    fn.argtypes, fn.restype = [ctypes.c_float], ctypes.c_int
+    rng = np.random.default_rng(70)
+    vals = np.concatenate([np.abs(rng.standard_normal(20000)).astype(np.float32) * np.float32(10.0) ** rng.integers(-40, 38, 20000).astype(np.float32),
+                           np.array([448.0, 449.0, 1.75, 1.7500001, 0.0, 1e-45, 3e38, 224.0], np.float32)])
+    for v in vals[np.isfinite(vals)]:
+        assert fn(float(v)) == orc.lib().orc_mxfp8_exponent(float(v)), v

@@ -373,3 +373,152 @@ def test_qmatmul_ref_fp8_equals_exact_dot(orc):
     out, mag = orc.qmatmul_ref(1, xb, codes.astype(np.uint8), scales, size, rows, [0, 1], batch)
     np.testing.assert_array_equal(out.reshape(batch, rows), exact / 2.0 ** 19)
     np.testing.assert_array_equal(mag.reshape(batch, rows), (np.abs(n) @ np.abs(iv).T) / 2.0 ** 19)
+
+
+# ---------------------------------------------------------------------------
+# MXFP8 activations of the block-scaled path: shared exponent X =
+# ceil(log2(amax / 448)) (the smallest scale whose E4M3 range holds the block),
+# elements E4M3 nearest-even; the product reference dequantizes both operands.
+
+def _bf16_bits(x):
+    x = np.asarray(x, np.float32)
+    bits = x.view(np.uint32)
+    assert np.all(bits & 0xffff == 0), "value not exact in bf16"
+    return (bits >> 16).astype(np.uint16)
+
+
+def test_mxfp8_exponent_closed_form(orc):
+    """448 * 2^(X-1) < amax <= 448 * 2^X, and -127 at the bottom."""
+    rng = np.random.default_rng(47)
+    a = np.concatenate([np.abs(rng.standard_normal(4000)).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 4000),
+                        np.array([224.0, 448.0, np.nextafter(np.float32(448.0), np.float32(1e9)), 511.9, 512.0,
+                                  896.0, 1.0, 1.75, 1.7500001, 2.0 ** -119, 2.0 ** -120, 0.0], np.float32)])
+    for v in a[np.isfinite(a)]:
+        x = orc.lib().orc_mxfp8_exponent(float(v))
+        if float(v) <= math.ldexp(448.0, -127):
+            assert x == -127, v
+        else:
+            assert math.ldexp(448.0, x - 1) < float(v) <= math.ldexp(448.0, x), (v, x)
+    assert orc.lib().orc_mxfp8_exponent(448.0) == 0 and orc.lib().orc_mxfp8_exponent(449.0) == 1
+
+
+def _exact_mxfp8_rows(rng, rows, blocks, exps):
+    codes = rng.integers(0, 256, (rows, blocks, 32))
+    codes[(codes & 0x7f) == 0x7f] = 0x3c
+    X = rng.choice(exps, (rows, blocks))
+    pos = rng.integers(0, 32, (rows, blocks))
+    pos[:, 0], pos[:, -1] = 0, 31
+    for r in range(rows):
+        for b in range(blocks):
+            codes[r, b, pos[r, b]] = 0x7e | (0x80 * rng.integers(0, 2))
+    x = (E4M3_VAL[codes] * np.exp2(X)[:, :, None].astype(np.float64)).astype(np.float32)
+    return codes, X, x.reshape(rows, blocks * 32)
+
+
+def test_mxfp8_exact_blocks_roundtrip(orc):
+    """bf16 blocks of E4M3 values times 2^X with amax = 448 * 2^X quantize to
+    exactly those codes (-0 as +0) with scale byte X + 127 and dequantize back
+    bit for bit."""
+    rng = np.random.default_rng(48)
+    rows, blocks = 5, 16
+    codes, X, x = _exact_mxfp8_rows(rng, rows, blocks, np.concatenate([[-110, -1, 0, 1, 110], rng.integers(-60, 60, 6)]))
+    got_codes, got_scales = orc.quantize_mxfp8(_bf16_bits(x), rows, blocks * 32)
+    np.testing.assert_array_equal(got_scales.reshape(rows, blocks), X + 127)
+    np.testing.assert_array_equal(got_codes.reshape(rows, blocks, 32), np.where(codes == 0x80, 0, codes))
+    deq = E4M3_VAL[got_codes.reshape(rows, blocks, 32)] * np.exp2(X.astype(np.float64) - 0)[:, :, None]
+    np.testing.assert_array_equal(deq.astype(np.float32).reshape(rows, -1), x)
+
+
+def test_mxfp8_never_saturates_and_rounds_to_nearest(orc):
+    """A block maximum in (224, 448] * 2^X keeps X, so no element exceeds
+    448 after scaling; every element lands on its nearest E4M3 value (brute
+    force over the 127 magnitudes)."""
+    rng = np.random.default_rng(49)
+    rows, blocks = 4, 12
+    X = rng.integers(-40, 40, (rows, blocks))
+    t = rng.uniform(225.0, 448.0, (rows, blocks))
+    amax = t * np.exp2(X)
+    x = rng.uniform(-1.0, 1.0, (rows, blocks, 32)) * amax[:, :, None]
+    pos = rng.integers(0, 32, (rows, blocks))
+    for r in range(rows):
+        for b in range(blocks):
+            x[r, b, pos[r, b]] = amax[r, b]
+    xb = _bf16_bits(np.float32(x).view(np.uint32).__and__(0xffff0000).view(np.float32))
+    xf = (xb.astype(np.uint32) << 16).view(np.float32).reshape(rows, blocks, 32).astype(np.float64)
+    codes, scales = orc.quantize_mxfp8(xb, rows, blocks * 32)
+    codes = codes.reshape(rows, blocks, 32)
+    np.testing.assert_array_equal(scales.reshape(rows, blocks), X + 127)
+    scaled = xf / np.exp2(X)[:, :, None]
+    mags = np.abs(E4M3_VAL[:127])
+    target = np.minimum(np.abs(scaled), 448.0)
+    best = np.abs(target[..., None] - mags).min(axis=-1)
+    got = np.abs(E4M3_VAL[codes])
+    assert np.all(np.abs(got - target) == best)
+    assert np.all(np.abs(scaled) <= 448.0)
+    assert np.all((got == 0) | (np.sign(E4M3_VAL[codes]) == np.sign(scaled)))
+
+
+def test_mxfp8_zero_and_neighbouring_blocks(orc):
+    x = np.zeros((1, 128), np.float32)
+    x[0, 31] = 448.0 * 2 ** 20
+    x[0, 32:64] = -0.0
+    x[0, 64] = 448.0 * 2 ** -20
+    codes, scales = orc.quantize_mxfp8(_bf16_bits(x), 1, 128)
+    np.testing.assert_array_equal(scales, [20 + 127, 0, -20 + 127, 0])
+    assert codes[31] == 0x7e and codes[64] == 0x7e
+    assert np.all(codes[32:64] == 0) and np.all(codes[96:] == 0)
+
+
+def test_qsmatmul_ref_equals_exact_dot(orc):
+    """Exactly representable operands: the block-scaled reference equals the
+    integer-scaled dot product (MXFP4 and fp8 weights), and a row's scales
+    apply to that row only."""
+    rng = np.random.default_rng(50)
+    batch, size, rows = 3, 1024, 6
+    xc = rng.integers(0, 256, (batch, size))
+    xc[(xc & 0x7f) == 0x7f] = 0x41
+    xs = rng.integers(-3, 4, (batch, size // 32))
+    # a * 2^12 = (e4m3 * 2^9) * 2^(Xa + 3), an integer.
+    ia = np.rint(E4M3_VAL[xc] * 2 ** 9).astype(np.int64) * (1 << (np.repeat(xs, 32, axis=1) + 3))
+    wc = rng.integers(0, 16, (rows, size))
+    wx = rng.integers(-3, 4, (rows, size // 32))
+    # w * 2^4 = (2 e2m1) * 2^(Xw + 3), an integer.
+    iw = np.rint(2 * E2M1_VAL[wc]).astype(np.int64) * (1 << (np.repeat(wx, 32, axis=1) + 3))
+    packed = (wc[:, 0::2] | (wc[:, 1::2] << 4)).astype(np.uint8)
+    out, mag = orc.qsmatmul_ref(0, xc.astype(np.uint8), (xs + 127).astype(np.uint8), packed,
+                                (wx + 127).astype(np.uint8), size, rows, [0, 2], batch)
+    out, mag = out.reshape(batch, rows), mag.reshape(batch, rows)
+    exact = ia @ iw.T
+    np.testing.assert_array_equal(out[[0, 2]], exact[[0, 2]] / 2.0 ** 16)
+    np.testing.assert_array_equal(mag[[0, 2]], (np.abs(ia) @ np.abs(iw).T)[[0, 2]] / 2.0 ** 16)
+    assert np.all(np.isnan(out[1]))
+    # fp8 weights with power-of-two row scales.
+    wc8 = rng.integers(0, 256, (rows, size))
+    wc8[(wc8 & 0x7f) == 0x7f] = 0x23
+    k = rng.integers(-2, 3, rows)
+    iw8 = np.rint(E4M3_VAL[wc8] * 2 ** 9).astype(np.int64) * (1 << (k + 2))[:, None]
+    out8, _ = orc.qsmatmul_ref(1, xc.astype(np.uint8), (xs + 127).astype(np.uint8), wc8.astype(np.uint8),
+                               np.exp2(k.astype(np.float64)).astype(np.float32), size, rows, [0, 1, 2], batch)
+    np.testing.assert_array_equal(out8.reshape(batch, rows), (ia @ iw8.T) / 2.0 ** 23)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_qsmatmul_ref_matches_bf16_reference_on_exact_activations(orc, fmt):
+    """Activations that MXFP8 represents exactly quantize without error, so the
+    block-scaled reference equals the bf16-activation reference bit for bit."""
+    rng = np.random.default_rng(51 + fmt)
+    batch, size, rows = 2, 512, 9
+    _, _, x = _exact_mxfp8_rows(rng, batch, size // 32, rng.integers(-20, 20, 8))
+    xb = _bf16_bits(x)
+    xc, xs = orc.quantize_mxfp8(xb, batch, size)
+    w = (rng.standard_normal((rows, size)) / 16).astype(np.float32)
+    if fmt == 0:
+        c, s = orc.quantize_mxfp4(w, rows, size)
+        wc, ws = orc.pack_e2m1(c), s
+    else:
+        wc, ws = orc.quantize_fp8(w, rows, size)
+        ws = np.exp2(np.round(np.log2(ws))).astype(np.float32)  # power-of-two row scales: exact products
+    got, gmag = orc.qsmatmul_ref(fmt, xc, xs, wc, ws, size, rows, [0, 1], batch)
+    want, wmag = orc.qmatmul_ref(fmt, xb, wc, ws, size, rows, [0, 1], batch)
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(gmag, wmag)

@@ -1,0 +1,149 @@
+"""The block-scaled quantized-weight path on the GPU (l2c_matmul_qs): the
+device MXFP8 activation quantizer bit-exact with the oracle, and the
+contraction on the scaled matrix cores against the oracle's dequantize-both,
+double-accumulate reference within the implementation-check bound of
+experiments/blackwell/lowprec/spec.json:55-62 (gamma_K with u = 2^-23 times
+sum |terms|, plus u |reference|). The error against the bf16-activation
+reference (what activation quantization costs) is bounded by 2^-4 of sum
+|terms| per output by construction and reported."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+U = 2.0 ** -23
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def untile_scales(tiled, batch, cols):
+    """[cols/128][Bp][4] scale tiles to row-major [batch][cols/32]."""
+    bp = (batch + 3) // 4 * 4
+    t = tiled.reshape(cols // 128, bp, 4)
+    return np.ascontiguousarray(t.transpose(1, 0, 2).reshape(bp, cols // 32)[:batch]), t[:, batch:, :]
+
+
+def weights(torch, l2c, fmt, W, rows, cols):
+    if fmt == 0:
+        codes = torch.empty(rows * cols // 2, dtype=torch.uint8, device="cuda")
+        scales = torch.empty(rows * cols // 32, dtype=torch.uint8, device="cuda")
+        l2c.quantize_mxfp4(codes, scales, dev(torch, W), rows, cols)
+    else:
+        codes = torch.empty(rows * cols, dtype=torch.uint8, device="cuda")
+        scales = torch.empty(rows, dtype=torch.float32, device="cuda")
+        l2c.quantize_fp8(codes, scales, dev(torch, W), rows, cols)
+    return codes, scales
+
+
+def bf16_activations(torch, l2c, x):
+    xbf = torch.empty(x.size, dtype=torch.int16, device="cuda")
+    l2c.to_bf16(xbf, dev(torch, x), x.size)
+    return xbf
+
+
+@pytest.mark.parametrize("batch,cols", [(4, 128), (33, 1024), (256, 4096), (7, 384)])
+def test_quantize_mxfp8_exact(torch_gpu, l2c, orc, batch, cols):
+    torch = torch_gpu
+    print(f"case quantize_mxfp8 {batch}x{cols}", flush=True)
+    rng = np.random.default_rng(batch + cols)
+    x = (rng.standard_normal(batch * cols) * 0.7).astype(np.float32)
+    ties = np.array([448.0, 480.0, 464.0, 0.0, -0.0, 2.0 ** -9, 2.0 ** -10, 3 * 2.0 ** -11, 1e30, -1e-30,
+                     17.0, 18.0, 19.0, 255.0, 256.0, 257.0], np.float32)
+    x[:ties.size] = ties
+    x[32:64] = 0.0                       # a zero block
+    x[64:96] *= np.float32(1e-36)        # a block of bf16 subnormals and tiny normals
+    x[96:128] *= np.float32(1e35)        # a block near the top of the range
+    xbf = bf16_activations(torch, l2c, x)
+    ws = torch.full((l2c.mxfp8_workspace_bytes(batch, cols),), 0xA5, dtype=torch.uint8, device="cuda")
+    l2c.quantize_mxfp8(ws, xbf, batch, cols)
+    torch.cuda.synchronize()
+    codes, tiled = l2c.mxfp8_views(ws, batch, cols)
+    oc, osc = orc.quantize_mxfp8(xbf.cpu().numpy().view(np.uint16), batch, cols)
+    np.testing.assert_array_equal(codes.cpu().numpy(), oc)
+    got_scales, padding = untile_scales(tiled.cpu().numpy(), batch, cols)
+    np.testing.assert_array_equal(got_scales.reshape(-1), osc)
+    assert np.all(padding == 0)
+
+
+def check_qs(torch, l2c, orc, fmt, batch, size, rows, x, W, label):
+    print(f"case matmul_qs {label} fmt={fmt} {batch}x{size}x{rows}", flush=True)
+    xbf = bf16_activations(torch, l2c, x)
+    codes, scales = weights(torch, l2c, fmt, W, rows, size)
+    ws = torch.empty(l2c.mxfp8_workspace_bytes(batch, size), dtype=torch.uint8, device="cuda")
+    out = torch.full((batch * rows,), float("nan"), dtype=torch.float32, device="cuda")
+    l2c.matmul_qs(out, xbf, codes, scales, fmt, batch, size, rows, ws)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    xb = xbf.cpu().numpy().view(np.uint16)
+    oc, osc = orc.quantize_mxfp8(xb, batch, size)
+    dc, dt = l2c.mxfp8_views(ws, batch, size)
+    np.testing.assert_array_equal(dc.cpu().numpy(), oc)  # the activations the product used
+    np.testing.assert_array_equal(untile_scales(dt.cpu().numpy(), batch, size)[0].reshape(-1), osc)
+    vec = list(range(batch))
+    wc, wsc = codes.cpu().numpy(), scales.cpu().numpy()
+    ref, mag = orc.qsmatmul_ref(fmt, oc, osc, wc, wsc, size, rows, vec, batch)
+    assert np.all(np.isfinite(got))
+    err = np.abs(got - ref)
+    gamma = size * U / (1 - size * U)
+    bad = err > gamma * mag + U * np.abs(ref) + 1e-30
+    assert not np.any(bad), (np.argwhere(bad.reshape(batch, rows))[:5], got[bad][:5], ref[bad][:5])
+    # Against the bf16-activation reference: E4M3 keeps 4 significant bits, so
+    # each term moves by at most 2^-4 of itself.
+    ref16, mag16 = orc.qmatmul_ref(fmt, xb, wc, wsc, size, rows, vec, batch)
+    rel16 = np.max(np.abs(got - ref16) / np.maximum(mag16, 1e-30))
+    print(f"  max |p - ref_bf16| / sum|terms| = {rel16:.3e}; max err / bound = "
+          f"{np.max(err / (gamma * mag + U * np.abs(ref) + 1e-30)):.3f}", flush=True)
+    assert rel16 <= 2.0 ** -4 * (1 + 1e-6)
+    # Deterministic: a second call gives the same bits.
+    again = torch.full((batch * rows,), float("nan"), dtype=torch.float32, device="cuda")
+    l2c.matmul_qs(again, xbf, codes, scales, fmt, batch, size, rows, ws)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(again.cpu().numpy().view(np.uint32), out.cpu().numpy().view(np.uint32))
+    return rel16
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+# One k-step (128), two, three (as many as the DMA ring has stages), ragged
+# tiles on both axes, batches that are not a multiple of 4 (padded scale
+# rows), and grids of many tiles with the XCD-ordered tile map.
+@pytest.mark.parametrize("batch,size,rows", [(8, 128, 16), (5, 128, 9), (3, 256, 5), (9, 384, 17),
+                                             (300, 1024, 200), (33, 384, 77), (256, 4096, 256),
+                                             (520, 1152, 1030), (1024, 2048, 1024)])
+def test_matmul_qs(torch_gpu, l2c, orc, fmt, batch, size, rows):
+    inp = orc.fill("normal", 6, batch, size, rows)
+    check_qs(torch_gpu, l2c, orc, fmt, batch, size, rows, inp.input, inp.matrix, "normal")
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_matmul_qs_scale_spread(torch_gpu, l2c, orc, fmt):
+    """Blocks of activations and weights whose magnitudes differ by up to
+    2^+-12 within a row, zero blocks and tiny blocks: every scale byte class
+    the realistic operands reach, to the same bound."""
+    batch, size, rows = 64, 1024, 96
+    rng = np.random.default_rng(60 + fmt)
+    x = rng.standard_normal((batch, size // 32, 32))
+    x *= np.exp2(rng.integers(-12, 13, (batch, size // 32, 1)))
+    x[::7, 3] = 0.0
+    W = rng.standard_normal((rows, size // 32, 32))
+    W *= np.exp2(rng.integers(-12, 13, (rows, size // 32, 1)))
+    W[::5, 6] = 0.0
+    check_qs(torch_gpu, l2c, orc, fmt, batch, size, rows, x.astype(np.float32).reshape(-1),
+             W.astype(np.float32).reshape(-1), "spread")
+
+
+def test_matmul_qs_rejects_bad_arguments(torch_gpu, l2c):
+    """cols % 128 != 0, a short workspace and a misaligned scale pointer are
+    refused before anything is launched."""
+    torch = torch_gpu
+    lib = l2c.load()
+    buf = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    p = buf.data_ptr()
+    s = torch.cuda.current_stream().cuda_stream
+    need = l2c.mxfp8_workspace_bytes(64, 1024)
+    assert l2c.mxfp8_workspace_bytes(64, 1000) == 0
+    assert lib.l2c_matmul_qs(p, p, p, p, 0, 64, 1000, 64, p, 1 << 20, s) == 1
+    assert lib.l2c_matmul_qs(p, p, p, p, 0, 64, 1024, 64, p, need - 1, s) == 1
+    assert lib.l2c_matmul_qs(p, p, p, p + 2, 0, 64, 1024, 64, p, need, s) == 1
+    assert lib.l2c_matmul_qs(p, p, p, p, 2, 64, 1024, 64, p, need, s) == 1
