@@ -52,9 +52,18 @@
 //    clamped per lane to the last row, scale words past the padded rows to
 //    the last four rows; those rows are computed and never stored.
 //  * Workgroup order is remapped per XCD as in the other contractions.
+#include <mutex>
+
 #include "l2c_common.h"
 #include "l2c_formats.h"
 #include "../../include/l2c.h"
+
+// Fixed scratch of l2c_matmul_qs_static: the MXFP8 activations of one call.
+// Each GPU the library runs on holds its own copy until the process ends.
+// In host code `scratch` is only a stand-in for the symbol: its device
+// address comes from hipGetSymbolAddress (per device, below), and only that
+// address is passed to kernels.
+static __device__ __align__(256) uint8_t scratch[L2C_QS_STATIC_SCRATCH_BYTES];
 
 namespace {
 
@@ -419,6 +428,43 @@ extern "C" int l2c_matmul_qs(float *out, const void *Xbf16, const void *Wq, cons
                        out, v.codes, v.scales, W, scales, batch, rows, cols);
   L2C_LAUNCH_CHECK();
   return hipSuccess;
+}
+
+namespace {
+
+// Device address of `scratch` on each device, resolved once per device with
+// that device current.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void *g_scratch[kMaxDevices] = {};
+
+int scratch_on_current_device(void **ptr) {
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return e;
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> hold(g_scratch_lock);
+  if (!g_scratch[device]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch[device] = p;
+  }
+  *ptr = g_scratch[device];
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int l2c_matmul_qs_static(float *out, const void *Xbf16, const void *Wq, const void *scales, int fmt,
+                                    int batch, int cols, int rows, hipStream_t stream) {
+  if (const int e = check_shape(batch, cols, rows)) return e;
+  if (batch == 0 || rows == 0) return l2c_matmul_qs(out, Xbf16, Wq, scales, fmt, batch, cols, rows, nullptr, 0, stream);
+  const size_t need = l2c_mxfp8_workspace_bytes(batch, cols);
+  if (need == 0 || need > static_cast<size_t>(L2C_QS_STATIC_SCRATCH_BYTES)) return hipErrorInvalidValue;
+  void *ws = nullptr;
+  if (const int e = scratch_on_current_device(&ws)) return e;
+  return l2c_matmul_qs(out, Xbf16, Wq, scales, fmt, batch, cols, rows, ws, L2C_QS_STATIC_SCRATCH_BYTES, stream);
 }
 
 int l2c_scgemm_occupancy(int fmt, int *blocks_per_cu) {

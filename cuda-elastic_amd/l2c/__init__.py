@@ -45,8 +45,9 @@ KERNEL_SYMBOLS = (
     "l2c_decoder_init_model", "l2c_decoder_rmsnorm", "l2c_decoder_softmax_argmax",
     "l2c_quantize_mxfp6", "l2c_nvfp4_tensor_scales", "l2c_quantize_nvfp4", "l2c_to_bf16_x4",
     "l2c_matmul_bf16", "l2c_matmul_mxfp6", "l2c_mxfp6_bytes",
-    "l2c_matmul_qs", "l2c_quantize_mxfp8", "l2c_mxfp8_workspace_bytes",
+    "l2c_matmul_qs", "l2c_quantize_mxfp8", "l2c_mxfp8_workspace_bytes", "l2c_matmul_qs_static",
 )
+QS_STATIC_SCRATCH_BYTES = 24 << 20  # L2C_QS_STATIC_SCRATCH_BYTES
 NVFP4_PARTIALS = 1024  # L2C_NVFP4_PARTIALS
 HOST_SYMBOLS = ("l2c_harness_main", "l2c_compare_dumps", "l2c_decoder_main", "l2c_decoder_run",
                 "l2c_lowprec_main", "l2c_lowprec_run", "l2c_lowprec_host_quantize", "l2c_lowprec_fixture",
@@ -106,6 +107,7 @@ def load() -> ctypes.CDLL:
         "l2c_matmul_mxfp6": [p, p, p, p, p, i, i, i, p],
         "l2c_matmul_qs": [p, p, p, p, i, i, i, i, p, sz, p],
         "l2c_quantize_mxfp8": [p, sz, p, i, i, p],
+        "l2c_matmul_qs_static": [p, p, p, p, i, i, i, i, p],
     }
     for name, args in sigs.items():
         fn = getattr(lib, name)
@@ -232,6 +234,11 @@ def matmul_qs(out, xbf16, wq, scales, fmt, batch, cols, rows, workspace, stream=
     _check(load().l2c_matmul_qs(_vp(_ptr(out)), _vp(_ptr(xbf16)), _vp(_ptr(wq)), _vp(_ptr(scales)), fmt, batch,
                                 cols, rows, _vp(_ptr(workspace)), workspace.numel() * workspace.element_size(),
                                 _vp(_stream(stream))), "l2c_matmul_qs")
+
+
+def matmul_qs_static(out, xbf16, wq, scales, fmt, batch, cols, rows, stream=None):
+    _check(load().l2c_matmul_qs_static(_vp(_ptr(out)), _vp(_ptr(xbf16)), _vp(_ptr(wq)), _vp(_ptr(scales)), fmt,
+                                       batch, cols, rows, _vp(_stream(stream))), "l2c_matmul_qs_static")
 
 
 def quantize_mxfp8(workspace, xbf16, batch, cols, stream=None):

@@ -147,6 +147,24 @@ int l2c_quantize_mxfp8(void *workspace, size_t workspace_bytes, const uint16_t *
 size_t l2c_mxfp8_workspace_bytes(int batch, int cols);
 
 /*
+ * l2c_matmul_qs without a workspace argument and without any allocation: the
+ * MXFP8 activations go to a fixed scratch array inside the library
+ * (L2C_QS_STATIC_SCRATCH_BYTES per GPU, held until the process ends; its
+ * device address is looked up once per device on the first call there). No
+ * counterpart in the reference: this entry point is for callers that cannot
+ * allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Returns hipErrorInvalidValue when
+ * l2c_mxfp8_workspace_bytes(batch, cols) exceeds the scratch size (batch *
+ * cols up to about 24.4 million; the benchmark shape 1024 x 16384 needs
+ * 16.5 MiB). Results equal l2c_matmul_qs's bit for bit. Every call on one GPU
+ * uses that GPU's single scratch: calls that may overlap on one GPU (other
+ * streams, other host threads) race and must be ordered by the caller.
+ */
+#define L2C_QS_STATIC_SCRATCH_BYTES (24u << 20)
+int l2c_matmul_qs_static(float *out, const void *Xbf16, const void *Wq, const void *scales, int fmt,
+                         int batch, int cols, int rows, hipStream_t stream);
+
+/*
  * Quantizers for l2c_matmul_q's weight operand, run on the device (setup work,
  * outside any timed region):
  *   l2c_quantize_mxfp4: codes[r][k/2] (cols/2 bytes per row), scales[r][k/32];
