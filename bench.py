@@ -7,7 +7,8 @@ headline workload is the largest profiled shape, batch 1024 x dim 16384 x rows
 hipGraph, no copies: `value` is its microseconds per iteration (lower is
 better). The other benchmark configurations (decode GEMV 1 x 4096 x 11008,
 launch-bound 8 x 768 x 2048, the reference-compatible GEMV iteration at the
-large shape, the fused single launch, the MXFP4 / fp8 weights, and the
+large shape, the fused single launch, the MXFP4 / fp8 weights on the bf16
+matrix cores and on the block-scaled fp8 matrix cores (MXFP8 activations), and the
 loom-private llama2c decoder application at its large shape, and the lowprec
 classifier experiment's fp32 / bf16 / MXFP6 / NVFP4 cases at that shape) and
 the graph/direct and copy/nocopy splits are reported under "lines".
@@ -65,7 +66,13 @@ def summarize(name, rec):
         "matmul_bound": rec["matmul_bound"], "matmul_frac": rec["matmul_frac"],
         "rms_max_rel_err": rec["rms_max_rel_err"], "softmax_max_rel_err": rec["softmax_max_rel_err"],
         "product_max_rel_err": rec["product_max_rel_err"],
+        "matmul_within_iter": rec.get("matmul_within_iter"),
     }
+    if rec["matmul"] in ("mxfp4s", "fp8s"):
+        # Block-scaled products: matmul_frac is against the 5.0 PFLOP/s dense
+        # fp8 matrix peak; the error against the bf16-activation reference is
+        # what quantizing the activations to MXFP8 costs (configuration: 2e-3).
+        out["product_bf16_act_rel_err"] = rec["product_bf16_act_rel_err"]
     if rec["mode"] == "graph":
         out["graph_capture_ms"] = rec["graph_capture_ms"]
         out["graph_instantiate_ms"] = rec["graph_instantiate_ms"]
@@ -268,7 +275,7 @@ def main():
             ("c3_fused_direct_nocopy", cfg("direct", 10000, 8, 768, 2048, "nocopy", "fused", warm=100)),
             ("c3_fused_direct_copy", cfg("direct", 10000, 8, 768, 2048, "copy", "fused", warm=100)),
         ]
-        for fmt in ("mxfp4", "fp8"):
+        for fmt in ("mxfp4", "fp8", "mxfp4s", "fp8s"):
             for mode in ("graph", "direct"):
                 for copies in ("nocopy", "copy"):
                     plan.append((f"c5_{fmt}_{mode}_{copies}",

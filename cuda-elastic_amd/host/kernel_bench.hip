@@ -18,6 +18,12 @@
 // once, written once): the calibration kernel for the FETCH_SIZE/WRITE_SIZE
 // counters.
 //
+// `gemv_cold` times the coalesced matrix-vector product with the 256 MB
+// Infinity Cache (MALL) flushed before every launch: a copy of 1 GiB runs
+// between launches and only the product is bracketed by events, so its time
+// is HBM's rate for W, not a MALL hit's (`gemv` runs back to back, where a W
+// of up to ~256 MB stays in the MALL between launches).
+//
 //   l2c_kernel_bench ceiling
 // measures the matrix-core rate the contractions can reach: register-only
 // loops (no memory traffic) of v_mfma_f32_32x32x2_f32, v_mfma_f32_32x32x16_bf16
@@ -340,6 +346,30 @@ int main(int argc, char **argv) {
   hipEvent_t t0, t1;
   CHECK(hipEventCreate(&t0));
   CHECK(hipEventCreate(&t1));
+  if (op == "gemv_cold") {
+    constexpr size_t kFlush = size_t(512) << 20;  // two 512 MiB buffers: 1 GiB moved per flush
+    float4 *fa = nullptr, *fb = nullptr;
+    CHECK(hipMalloc(&fa, kFlush));
+    CHECK(hipMalloc(&fb, kFlush));
+    CHECK(hipMemset(fa, 0, kFlush));
+    double total_ms = 0.0;
+    for (int i = 0; i < iters + 3; ++i) {
+      hipLaunchKernelGGL(copy_kernel, dim3(4096), dim3(256), 0, s, fb, fa, kFlush / 16);
+      CHECK(hipGetLastError());
+      CHECK(hipEventRecord(t0, s));
+      L2C(l2c_matvec(prod, x, m, S, R, L2C_MATVEC_COALESCED, s));
+      CHECK(hipEventRecord(t1, s));
+      CHECK(hipEventSynchronize(t1));
+      float ms = 0.0f;
+      CHECK(hipEventElapsedTime(&ms, t0, t1));
+      if (i >= 3) total_ms += ms;  // three untimed rounds first
+    }
+    const double us = 1000.0 * total_ms / iters;
+    const double bytes = mat * 4.0 + (S + static_cast<double>(R)) * 4;
+    std::printf("op=%s batch=%d size=%d rows=%d iters=%d avg_us=%.3f bytes=%.0f gbps=%.1f\n", op.c_str(), B, S, R,
+                iters, us, bytes, bytes / (us * 1e3));
+    return 0;
+  }
   // Warm-up of 100 ms (at least 3 and at most 1000 launches): the matrix cores reach their
   // steady clock only after some tens of milliseconds under load.
   int warm = 0;

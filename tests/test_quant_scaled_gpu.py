@@ -147,3 +147,40 @@ def test_matmul_qs_rejects_bad_arguments(torch_gpu, l2c):
     assert lib.l2c_matmul_qs(p, p, p, p, 0, 64, 1024, 64, p, need - 1, s) == 1
     assert lib.l2c_matmul_qs(p, p, p, p + 2, 0, 64, 1024, 64, p, need, s) == 1
     assert lib.l2c_matmul_qs(p, p, p, p, 2, 64, 1024, 64, p, need, s) == 1
+
+
+@pytest.mark.parametrize("shift", [0, 10])
+def test_quantize_mxfp8_every_bf16_value(torch_gpu, l2c, orc, shift):
+    """Every bf16 value of magnitude <= 448 (both signs, subnormals, zeros),
+    31 to a block beside a 448 * 2^shift that fixes the block's scale, times
+    2^shift: the device codes (the hardware E4M3 conversion) equal the
+    oracle's nearest-even encoder at every one, ties and -0 included."""
+    torch = torch_gpu
+    mags = np.arange(0, 0x43E1, dtype=np.uint32)            # bf16 patterns 0 .. 448
+    vals = np.concatenate([mags, mags | 0x8000]).astype(np.uint32) << 16
+    v = vals.view(np.float32).astype(np.float64) * 2.0 ** shift
+    per = 31
+    nblk = -(-v.size // per)
+    blocks = np.zeros((nblk, 32))
+    blocks[:, 0] = 448.0 * 2.0 ** shift
+    flat = np.zeros(nblk * per)
+    flat[:v.size] = v
+    blocks[:, 1:] = flat.reshape(nblk, per)
+    x = blocks.reshape(-1)
+    cols = 128 * 64
+    rows = -(-x.size // cols)
+    x = np.concatenate([x, np.zeros(rows * cols - x.size)]).astype(np.float32)
+    xb = (x.view(np.uint32) >> 16).astype(np.uint16)
+    assert np.array_equal((xb.astype(np.uint32) << 16).view(np.float32), x)  # exact in bf16
+    print(f"case quantize_mxfp8 every bf16 value, shift {shift}, {rows}x{cols}", flush=True)
+    xbf = torch.from_numpy(xb.view(np.int16)).cuda()
+    ws = torch.empty(l2c.mxfp8_workspace_bytes(rows, cols), dtype=torch.uint8, device="cuda")
+    l2c.quantize_mxfp8(ws, xbf, rows, cols)
+    torch.cuda.synchronize()
+    codes, tiled = l2c.mxfp8_views(ws, rows, cols)
+    oc, osc = orc.quantize_mxfp8(xb, rows, cols)
+    assert np.all(osc[:nblk] == 127 + shift)  # each block's 448 * 2^shift sets its scale
+    got = codes.cpu().numpy()
+    bad = np.flatnonzero(got != oc)
+    assert bad.size == 0, (bad[:8], x[bad[:8]], got[bad[:8]], oc[bad[:8]])
+    np.testing.assert_array_equal(untile_scales(tiled.cpu().numpy(), rows, cols)[0].reshape(-1), osc)
