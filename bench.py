@@ -67,6 +67,7 @@ def summarize(name, rec):
         "rms_max_rel_err": rec["rms_max_rel_err"], "softmax_max_rel_err": rec["softmax_max_rel_err"],
         "product_max_rel_err": rec["product_max_rel_err"],
         "matmul_within_iter": rec.get("matmul_within_iter"),
+        "one_stream": rec.get("one_stream"), "host_write": rec.get("host_write"),
     }
     if rec["matmul"] in ("mxfp4s", "fp8s"):
         # Block-scaled products: matmul_frac is against the 5.0 PFLOP/s dense
@@ -275,11 +276,35 @@ def main():
             ("c3_fused_direct_nocopy", cfg("direct", 10000, 8, 768, 2048, "nocopy", "fused", warm=100)),
             ("c3_fused_direct_copy", cfg("direct", 10000, 8, 768, 2048, "copy", "fused", warm=100)),
         ]
+        # Iteration forms beyond the reference protocol: one stream without
+        # fork/join events, and copy-mode downloads by device stores into the
+        # pinned host buffers (hostwrite) in place of memcpy nodes / calls.
+        plan += [
+            ("c3_onestream_graph_nocopy", cfg("graph", 10000, 8, 768, 2048, "nocopy", "coalesced", warm=100,
+                                              extra=("onestream",))),
+            ("c3_onestream_direct_nocopy", cfg("direct", 10000, 8, 768, 2048, "nocopy", "coalesced", warm=100,
+                                               extra=("onestream",))),
+            ("c3_onestream_graph_copy", cfg("graph", 10000, 8, 768, 2048, "copy", "coalesced", warm=100,
+                                            extra=("onestream",))),
+            ("c3_graph_copy_hostwrite", cfg("graph", 10000, 8, 768, 2048, "copy", "coalesced", warm=100,
+                                            extra=("hostwrite",))),
+            ("c3_direct_copy_hostwrite", cfg("direct", 10000, 8, 768, 2048, "copy", "coalesced", warm=100,
+                                             extra=("hostwrite",))),
+            ("c2_onestream_graph_nocopy", cfg("graph", 1000, 1, 4096, 11008, "nocopy", "coalesced", warm=50,
+                                              extra=("onestream",))),
+            ("c2_onestream_direct_nocopy", cfg("direct", 1000, 1, 4096, 11008, "nocopy", "coalesced", warm=50,
+                                               extra=("onestream",))),
+            ("c4_batched_graph_copy_hostwrite", cfg("graph", K, B, S, R, "copy", "batched", extra=("hostwrite",))),
+            ("c4_batched_direct_copy_hostwrite", cfg("direct", K, B, S, R, "copy", "batched", extra=("hostwrite",))),
+            ("c4_batched_onestream_graph_nocopy", cfg("graph", K, B, S, R, "nocopy", "batched", extra=("onestream",))),
+        ]
         for fmt in ("mxfp4", "fp8", "mxfp4s", "fp8s"):
             for mode in ("graph", "direct"):
                 for copies in ("nocopy", "copy"):
                     plan.append((f"c5_{fmt}_{mode}_{copies}",
                                  cfg(mode, K, B, S, R, copies, fmt, inputs="normal=1")))
+            plan.append((f"c5_{fmt}_onestream_graph_nocopy",
+                         cfg("graph", K, B, S, R, "nocopy", fmt, inputs="normal=1", extra=("onestream",))))
         for name, a in plan:
             lines.append(summarize(name, run_line(l2c, a)))
         for mode in ("graph", "direct"):

@@ -59,7 +59,8 @@ std::string usage_text(const char *program) {
   text +=
       " [graph|direct] [launches|auto] [batch] [size] [rows] [repeats] [warmup_ms]"
       " [copy|nocopy] [naive|coalesced|fused|batched|mxfp4|fp8|mxfp4s|fp8s]"
-      " [deterministic|random[=SEED]|scaled[=SEED]|normal[=SEED]] [fullcheck] [warmup_iters=N]"
+      " [deterministic|random[=SEED]|scaled[=SEED]|normal[=SEED]] [fullcheck] [onestream] [hostwrite]"
+      " [warmup_iters=N]"
       " [--dump=FILE]\n";
   return text;
 }
@@ -124,7 +125,7 @@ bool parse_options(int argc, const char *const *argv, Options *options, std::str
     if (input > 0) continue;
     struct Word {
       const char *name;
-      int kind;  // 0 graph, 1 direct, 2 nocopy, 3 copy, 4 matmul, 5 fullcheck
+      int kind;  // 0 graph, 1 direct, 2 nocopy, 3 copy, 4 matmul, 5 fullcheck, 6 onestream, 7 hostwrite
       Matmul matmul;
     };
     static const Word words[] = {
@@ -134,7 +135,8 @@ bool parse_options(int argc, const char *const *argv, Options *options, std::str
         {"fused", 4, Matmul::kFused},         {"batched", 4, Matmul::kBatched},
         {"mxfp4", 4, Matmul::kMxfp4},         {"fp8", 4, Matmul::kFp8},
         {"mxfp4s", 4, Matmul::kMxfp4s},       {"fp8s", 4, Matmul::kFp8s},
-        {"fullcheck", 5, Matmul::kNaive}};
+        {"fullcheck", 5, Matmul::kNaive},     {"onestream", 6, Matmul::kNaive},
+        {"hostwrite", 7, Matmul::kNaive}};
     bool matched = false;
     for (const Word &w : words) {
       if (std::strcmp(arg, w.name) != 0) continue;
@@ -146,6 +148,8 @@ bool parse_options(int argc, const char *const *argv, Options *options, std::str
         case 3: options->copy_outputs = true; break;
         case 4: options->matmul = w.matmul; break;
         case 5: options->full_check = true; break;
+        case 6: options->one_stream = true; break;
+        case 7: options->host_write = true; break;
       }
       break;
     }

@@ -66,6 +66,10 @@ struct Options {
   bool auto_launches = false;
   bool full_check = false;  // validate every (b, r) of a batched product
   int warmup_iters = 0;     // > 0: exactly this many warm-up iterations instead of warmup_ms
+  // Iteration forms beyond the reference protocol (llama2c_cuda_graph.cu:347-381):
+  bool one_stream = false;  // every launch and copy on one stream, no fork/join events
+  bool host_write = false;  // copy mode: a device kernel stores the outputs into the
+                            // pinned host buffers in place of hipMemcpyAsync
   int device = 0;
   InputOptions inputs;
 };

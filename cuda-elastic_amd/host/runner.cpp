@@ -279,9 +279,18 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
       L2C_OK(l2c_fused(d_normalized.ptr, d_input.ptr, d_weight.ptr, d_softmax.ptr, d_prob.ptr,
                        d_product.ptr, d_matrix.ptr, S, rms_rows, soft_rows, mm_rows, kRmsEpsilon, s));
     };
+    // Copy-mode downloads: hipMemcpyAsync as the reference does, or (hostwrite)
+    // a kernel storing into the pinned host buffers.
     auto d2h = [&](float *dst, const float *src, size_t n, hipStream_t s) {
-      HIP_OK(hipMemcpyAsync(dst, src, n * 4, hipMemcpyDeviceToHost, s));
+      if (o.host_write) L2C_OK(l2c_copy_to_host(dst, src, n * 4, s));
+      else HIP_OK(hipMemcpyAsync(dst, src, n * 4, hipMemcpyDeviceToHost, s));
     };
+    // Kernels one iteration launches (the block-scaled products launch their
+    // activation quantizer too; hostwrite adds one kernel per download).
+    const int kernels_per_rep = mm == Matmul::kFused ? 1 : 3 + (scaled ? 1 : 0);
+    const int kernels_per_iter_planned =
+        kernels_per_rep * o.repeats +
+        (o.copy_outputs ? (o.host_write ? 3 : 0) + (mm == Matmul::kFused && !o.one_stream ? 1 : 0) : 0);
 
     // One iteration. Three-stream variants: fork from the rmsnorm stream,
     // `repeats` x {rmsnorm | softmax | matmul} on their streams, copies on
@@ -289,14 +298,32 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
     // Fused: one launch per repeat; in copy mode the last repeat runs the
     // rmsnorm rows first so their copy overlaps the softmax and matmul rows
     // on the side stream (llama2c_sota.cu:474-496).
+    // onestream: the same work on the rmsnorm stream alone, in the same order,
+    // with no fork/join events (an iteration form beyond the reference's).
     int kernels_per_iter = 0;
     auto enqueue_iteration = [&]() {
-      kernels_per_iter = 0;
+      kernels_per_iter = kernels_per_iter_planned;
+      if (o.one_stream) {
+        for (int rep = 0; rep < o.repeats; ++rep) {
+          if (mm == Matmul::kFused) {
+            fused(B, B, R, st.rms);
+          } else {
+            launch_matmul(st.rms);
+            launch_rms(st.rms);
+            launch_softmax(st.rms);
+          }
+        }
+        if (o.copy_outputs) {
+          d2h(h_normalized.ptr, d_normalized.ptr, vec_elems, st.rms);
+          d2h(h_softmax.ptr, d_softmax.ptr, vec_elems, st.rms);
+          d2h(h_product.ptr, d_product.ptr, prod_elems, st.rms);
+        }
+        return;
+      }
       if (mm == Matmul::kFused) {
         for (int rep = 0; rep < o.repeats; ++rep) {
           if (!(o.copy_outputs && rep + 1 == o.repeats)) {
             fused(B, B, R, st.rms);
-            ++kernels_per_iter;
             continue;
           }
           HIP_OK(hipEventRecord(st.fork, st.rms));
@@ -308,7 +335,6 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
           d2h(h_product.ptr, d_product.ptr, prod_elems, st.soft);
           HIP_OK(hipEventRecord(st.soft_done, st.soft));
           HIP_OK(hipStreamWaitEvent(st.rms, st.soft_done, 0));
-          kernels_per_iter += 2;
         }
         return;
       }
@@ -322,7 +348,6 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
         launch_matmul(st.mm);
         launch_rms(st.rms);
         launch_softmax(st.soft);
-        kernels_per_iter += 3;
         if (rep + 1 == o.repeats && o.copy_outputs) {
           d2h(h_normalized.ptr, d_normalized.ptr, vec_elems, st.rms);
           d2h(h_softmax.ptr, d_softmax.ptr, vec_elems, st.soft);
@@ -351,8 +376,7 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
       HIP_OK(hipStreamSynchronize(st.rms));
       res->graph_upload_ms = ms_since(t);
     } else {
-      // Count the launches of one iteration without running it.
-      kernels_per_iter = mm == Matmul::kFused ? o.repeats + (o.copy_outputs ? 1 : 0) : 3 * o.repeats;
+      kernels_per_iter = kernels_per_iter_planned;
     }
     res->kernels_per_iter = kernels_per_iter;
 
@@ -522,7 +546,7 @@ std::string result_line(const Options &o, const RunResult &r, const Validation &
       "softmax_gbps=%.1f softmax_hbm_frac=%.4f matmul_us=%.3f matmul_gbps=%.1f matmul_tflops=%.3f "
       "matmul_bound=%s matmul_frac=%.4f rms_max_rel_err=%.3e softmax_max_rel_err=%.3e "
       "product_max_rel_err=%.3e product_max_tol_ratio=%.3e check_vectors=%zu strict_valid=%d "
-      "matmul_within_iter=%d product_bf16_act_rel_err=%.3e",
+      "matmul_within_iter=%d product_bf16_act_rel_err=%.3e one_stream=%d host_write=%d",
       o.graph ? "graph" : "direct", matmul_name(o.matmul), r.launches, o.batch, o.size, o.rows,
       o.repeats, o.copy_outputs ? 1 : 0, o.warmup_ms, r.warmup_iterations, r.gpu_ms, gpu_ms_per_iter,
       kSingleIterations, r.single_us, r.wall_ms, r.wall_ms / r.launches, r.submit_us,
@@ -537,7 +561,8 @@ std::string result_line(const Options &o, const RunResult &r, const Validation &
       batched ? "mfma" : "hbm", mm_frac, v.rms_max_rel_error, v.softmax_max_rel_error,
       v.product_max_rel_error, v.product_max_ratio,
       batched ? v.product.sampled_batch_rows.size() : static_cast<size_t>(1), strict_valid ? 1 : 0,
-      r.matmul.us <= gpu_ms_per_iter * 1000.0 ? 1 : 0, v.product_bf16_act_rel_error);
+      r.matmul.us <= gpu_ms_per_iter * 1000.0 ? 1 : 0, v.product_bf16_act_rel_error, o.one_stream ? 1 : 0,
+      o.host_write ? 1 : 0);
   std::string line = buf;
   // Device names may contain spaces; keep the line space-separated key=value.
   const size_t d = line.find(" device=");

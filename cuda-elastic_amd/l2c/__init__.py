@@ -46,6 +46,7 @@ KERNEL_SYMBOLS = (
     "l2c_quantize_mxfp6", "l2c_nvfp4_tensor_scales", "l2c_quantize_nvfp4", "l2c_to_bf16_x4",
     "l2c_matmul_bf16", "l2c_matmul_mxfp6", "l2c_mxfp6_bytes",
     "l2c_matmul_qs", "l2c_quantize_mxfp8", "l2c_mxfp8_workspace_bytes", "l2c_matmul_qs_static",
+    "l2c_copy_to_host",
 )
 QS_STATIC_SCRATCH_BYTES = 24 << 20  # L2C_QS_STATIC_SCRATCH_BYTES
 NVFP4_PARTIALS = 1024  # L2C_NVFP4_PARTIALS
@@ -108,6 +109,7 @@ def load() -> ctypes.CDLL:
         "l2c_matmul_qs": [p, p, p, p, i, i, i, i, p, sz, p],
         "l2c_quantize_mxfp8": [p, sz, p, i, i, p],
         "l2c_matmul_qs_static": [p, p, p, p, i, i, i, i, p],
+        "l2c_copy_to_host": [p, p, sz, p],
     }
     for name, args in sigs.items():
         fn = getattr(lib, name)

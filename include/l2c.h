@@ -263,6 +263,18 @@ int l2c_decoder_softmax_argmax(float *probabilities, const float *logits, int *t
                                int *generated, int vocab, int batch, int steps, int step,
                                hipStream_t stream);
 
+/*
+ * bytes from device memory `src` to pinned host memory `host_dst`
+ * (hipHostMalloc; on ROCm its host address is also its device address),
+ * copied by a kernel that stores straight into host memory: the copy is a
+ * kernel node when captured into a hipGraph, not a memcpy node. No
+ * counterpart kernel in the reference, whose copy mode downloads with
+ * cudaMemcpyAsync (llama2c/llama2c_cuda_graph.cu:369-374); the harness's
+ * `hostwrite` token uses it in that place. 16-byte stores when both pointers
+ * are 16-byte aligned, byte stores for the rest.
+ */
+int l2c_copy_to_host(void *host_dst, const void *src, size_t bytes, hipStream_t stream);
+
 /* Operations named by l2c_launch_shape. */
 enum l2c_op {
   L2C_OP_RMSNORM = 0,

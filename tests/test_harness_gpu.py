@@ -182,3 +182,27 @@ def test_executable_line_format(l2c):
     got = [t.split("=")[0] for t in line.split()][:len(keys)]
     assert got == keys
     assert rec["min_bytes_per_iter"] == 2 * 8 * 768 * 4 + 768 * 4 + 2 * 8 * 768 * 4 + 2048 * 768 * 4 + (768 + 2048) * 4
+
+
+@pytest.mark.parametrize("variant", ["coalesced", "naive", "fused", "batched", "mxfp4s"])
+@pytest.mark.parametrize("form", [("onestream",), ("hostwrite",), ("onestream", "hostwrite")],
+                         ids=lambda f: "+".join(f))
+def test_iteration_forms(l2c, orc, tmp_path, variant, form):
+    """The iteration forms beyond the reference protocol (one stream with no
+    fork/join; copy mode downloading through device stores into pinned host
+    memory) are valid in graph and direct mode, copy and nocopy, and write the
+    same outputs bit for bit as the reference protocol on the same inputs."""
+    batch, size, rows = 40, 1024, 300
+    for mode in ("graph", "direct"):
+        for copies in ("nocopy", "copy"):
+            base = [mode, 3, batch, size, rows, 1, 1, copies, variant, "random=2"]
+            ref_dump, dump = str(tmp_path / "ref.bin"), str(tmp_path / "form.bin")
+            print("case", " ".join(map(str, base + list(form))), flush=True)
+            code, rec, raw = run(l2c, base + [f"--dump={ref_dump}"])
+            assert code == 0 and rec["valid"] == 1, raw
+            code, rec, raw = run(l2c, base + list(form) + [f"--dump={dump}"])
+            assert code == 0 and rec["valid"] == 1 and rec["strict_valid"] == 1, raw
+            assert rec["one_stream"] == ("onestream" in form) and rec["host_write"] == ("hostwrite" in form)
+            a, b = orc.read_dump(ref_dump), orc.read_dump(dump)
+            for key in ("normalized", "softmax", "product"):
+                np.testing.assert_array_equal(a[key].view(np.uint32), b[key].view(np.uint32))
