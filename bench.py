@@ -32,6 +32,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "cuda-elastic_amd"))
 
 HBM_PEAK_GBPS = 8000.0
+WARMUP_MS = 100  # the reference harness's default warm-up time (llama2c_cuda_graph.cu:43-53)
 FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_f32_mfma_c4_traffic.json")
@@ -231,9 +232,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    # 100 warm-up iterations (~0.2 s at the headline shape): the matrix cores
-    # need about that long under load to reach their steady clock, and the
-    # reference's own default warm-up is 100 ms (llama2c_cuda_graph.cu:43-53).
+    # Warm-up: at least W iterations and at least the reference protocol's
+    # default 100 ms (llama2c_cuda_graph.cu:43-53,409-431), whichever is
+    # longer; a few iterations alone leave the clocks ramping through the
+    # timed loop (its first ~30 ms run up to 12% slow at the headline shape).
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--quick", action="store_true", help="headline and cpu baseline only")
     ap.add_argument("--no-cpu", action="store_true")
@@ -251,7 +253,7 @@ def main():
     B, S, R = 1024, 16384, 8192
 
     def cfg(mode, launches, batch, size, rows, copies, matmul, inputs="scaled=1", warm=W, extra=()):
-        return [mode, launches, batch, size, rows, 1, 1, copies, matmul, inputs,
+        return [mode, launches, batch, size, rows, 1, WARMUP_MS, copies, matmul, inputs,
                 f"warmup_iters={warm}", *extra]
 
     headline = run_line(l2c, cfg("graph", K, B, S, R, "nocopy", "batched"))
@@ -344,6 +346,8 @@ def main():
     result = {
         "metric": "us/iter (llama2c iteration: rmsnorm + softmax + batched fp32 W.x on MFMA), hipGraph",
         "value": us, "unit": "us/iter", "n_gpus": 1, "steps": headline["launches"], "warmup": W,
+        "warmup_protocol": {"min_iterations": W, "min_ms": WARMUP_MS,
+                            "iterations_run": headline["warmup_iterations"]},
         "ms_per_step": headline["gpu_ms_per_iter"], "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32",
         "data": "synthetic: seeded splitmix64 inputs, scaled distributions (x,logits U[-1,1), "

@@ -65,7 +65,7 @@ struct Options {
   Matmul matmul = Matmul::kNaive;
   bool auto_launches = false;
   bool full_check = false;  // validate every (b, r) of a batched product
-  int warmup_iters = 0;     // > 0: exactly this many warm-up iterations instead of warmup_ms
+  int warmup_iters = 0;     // > 0: at least this many warm-up iterations, and at least warmup_ms
   // Iteration forms beyond the reference protocol (llama2c_cuda_graph.cu:347-381):
   bool one_stream = false;  // every launch and copy on one stream, no fork/join events
   bool host_write = false;  // copy mode: a device kernel stores the outputs into the
