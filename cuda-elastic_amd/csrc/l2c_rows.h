@@ -250,27 +250,4 @@ __device__ inline void matvec_row_block_generic(float *out_elem, const float *mr
   if (threadIdx.x == 0) *out_elem = acc;
 }
 
-// Row loop shared by the rmsnorm and softmax kernels: block b handles rows
-// b, b + G, b + 2G, ... (G = gridDim.x). The next row's loads are issued
-// before the current row is reduced and stored, so one block keeps HBM busy
-// through its reductions. LDS slot sets alternate between rows: a set is
-// rewritten only after every lane has passed the next row's barrier.
-template <int V, bool VEC, bool EXACT, typename Apply>
-__device__ __forceinline__ void row_loop(const float *in, float *out, int size, int batch,
-                                         float fill, float *slots, Apply apply) {
-  int row = blockIdx.x;
-  if (row >= batch) return;
-  Row<V, VEC, EXACT> cur;
-  cur.load(in + static_cast<size_t>(row) * size, size, fill);
-  for (int parity = 0;; parity ^= 1) {
-    const int next = row + static_cast<int>(gridDim.x);
-    Row<V, VEC, EXACT> nxt;
-    if (next < batch) nxt.load(in + static_cast<size_t>(next) * size, size, fill);
-    apply(cur, out + static_cast<size_t>(row) * size, slots + 32 * parity);
-    if (next >= batch) break;
-    cur = nxt;
-    row = next;
-  }
-}
-
 }  // namespace l2c
