@@ -13,8 +13,9 @@
 //    the E8M0 byte shifted into that field is the scale for every byte value
 //    (byte 0, 0.0f, scales by 2^-127). The fp8 row scale multiplies each
 //    output in the epilogue.
-//  * Tile 256 (batch) x 128 (rows) x 64 (k per step), 8 wavefronts in k-slice
-//    pairs: waves w and w + 4 share a SIMD and a 128 x 64 output sub-tile and
+//  * Tile 256 (batch) x 128 (rows) x 64 (k per step) for MXFP4, 128 x 256 x 64
+//    for fp8, 8 wavefronts in k-slice pairs: waves w and w + 4 share a SIMD
+//    and a 128 x 64 output sub-tile (2 x 2 or 1 x 4 of them per group) and
 //    take the step's k-chunks 2g, 2g + 1 (g = w / 4); lane (r, h) of MFMA q
 //    supplies k = 32h + 8q + 0..7 for both operands, so a lane's codes for its
 //    two chunks are 8 contiguous bytes (MXFP4, one scale block h) or 16 (fp8).
@@ -28,13 +29,13 @@
 //    takes one wave's MFMAs while the other wave waits on LDS and memory.
 //    Group 1 takes one extra barrier at the start and group 0 one at the end,
 //    so every wave passes the same number of barriers.
-//  * LDS DMA staging (buffer_load ... lds): X 32 KB a step as 32 1-KB
-//    instructions (4 a wave); W codes 4 KB (MXFP4, waves 0-3) or 8 KB (fp8,
-//    one a wave); MXFP4 scales as 2-byte DMAs, one row a lane (waves 4, 5),
-//    each landing zero-extended in its own LDS word (a 2-byte DMA writes
-//    lane i's bytes at word i). Four stages (146 KB MXFP4, 160 KB fp8): a
-//    stage is free once both groups have read it, and a step's DMA has three
-//    steps to land.
+//  * LDS DMA staging (buffer_load ... lds): X 32 KB (MXFP4) or 16 KB (fp8) a
+//    step in 1-KB instructions of 8 rows; W codes 4 KB (MXFP4, waves 0-3) or
+//    16 KB (fp8, two a wave); MXFP4 scales as 2-byte DMAs, one row a lane
+//    (waves 4, 5), each landing zero-extended in its own LDS word (a 2-byte
+//    DMA writes lane i's bytes at word i). Four stages (146 KB MXFP4, 128 KB
+//    fp8): a stage is free once both groups have read it, and a step's DMA
+//    has three steps to land.
 //  * 16-byte chunks of LDS rows are XOR-swizzled by row bits (X: bits 1..3;
 //    W: bit 3 for 32-byte MXFP4 rows, bits 2..3 for 64-byte fp8 rows), applied
 //    on the DMA's source side, so the fragment reads avoid bank conflicts
@@ -46,10 +47,11 @@
 //    the DMA and the fragment reads 149 / 162 µs (the MFMAs alone on these
 //    operands); removing the conversions or the DMA wait changes nothing.
 //    Three stages for fp8 (128 KB, one step for the DMA) measured 213 µs.
-//    In the C5 iteration (rmsnorm and softmax on two more streams beside
-//    the product) MXFP4 runs 245 against 262 µs; fp8 277 against 262 µs:
-//    its product gets faster (225 against 260 µs on the harness's normal
-//    weights) but the row kernels no longer hide under it.
+//    fp8 on the 256 x 128 tile needed four 40 KB stages, the CU's whole
+//    LDS, so in the C5 iteration the row kernels could not run beside it.
+//    The 128 x 256 tile gives the same results bit for bit, in the same time
+//    alone (206.5 against 208.5 µs), with 32 KB stages; MXFP4 on it measured
+//    226 against 216 µs and keeps 256 x 128.
 //  * Every access is in bounds by construction: rows past the operand are
 //    clamped per lane to its last row; those rows are never stored.
 #include "l2c_common.h"
@@ -63,45 +65,80 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_ptr;
 
-constexpr int kBM = 256;
-constexpr int kBN = 128;
 constexpr int kThreads = 512;
 constexpr int kXcds = 8;
-constexpr int kXBytes = kBM * 128;    // 256 rows x 64 bf16
-constexpr int kExchange = 131072;     // 4 sub-tiles x 8 blocks x 16 values x 64 lanes x 4 B
+constexpr int kExchange = 131072;  // 4 sub-tiles x 8 blocks x 16 values x 64 lanes x 4 B
 
-template <int FMT, int STAGES>
+// A tile is BM batch rows x 32768 / BM weight rows (256 x 128 or 128 x 256); a
+// wave's sub-tile is always 128 x 64, so a wave group holds BM / 128 x BN / 64
+// of them.
+template <int FMT, int STAGES, int BM>
 struct Layout {
   static constexpr int kStages = STAGES;
   static constexpr bool kMx = FMT == L2C_Q_MXFP4;
-  static constexpr int kWRow = kMx ? 32 : 64;  // code bytes per W row and step
+  static constexpr int kBM = BM;
+  static constexpr int kBN = 32768 / BM;
+  static constexpr int kWavesM = BM / 128;        // sub-tiles along the batch
+  static constexpr int kXBytes = BM * 128;        // BM rows x 64 bf16
+  static constexpr int kXDma = BM / 64;           // X DMAs a wave issues a step (8 rows x 128 B each)
+  static constexpr int kWRow = kMx ? 32 : 64;     // code bytes per W row and step
   static constexpr int kLanesPerRow = kWRow / 16;
+  static constexpr int kWRowsPerDma = 64 / kLanesPerRow;
+  static constexpr int kWDma = kBN / kWRowsPerDma;  // W DMAs a step, instruction q on wave q % 8
+  static constexpr int kSDma = kMx ? kBN / 64 : 0;  // MXFP4 scale DMAs a step, on waves 4, 5, ...
   static constexpr int kSOff = kXBytes + kBN * kWRow;
   static constexpr int kStage = kSOff + (kMx ? kBN * 4 : 0);
   static constexpr int kLds = kStages * kStage > kExchange ? kStages * kStage : kExchange;
+  // The wait for a step's DMA lets STAGES - 2 newer steps stay in flight,
+  // counted at the fewest DMAs any wave issues a step (4 for the 256-row
+  // tile, whose waves issue 4 or 5; 4 for fp8 and 3 for MXFP4 on the 128-row
+  // tile): exact for those waves, stricter for the others.
+  static constexpr int kWait = (BM == 256 ? 4 : kXDma + kWDma / 8) * (STAGES - 2);
   static __device__ __forceinline__ int wswizzle(int row) { return kMx ? (row >> 3) & 1 : (row >> 2) & 3; }
 };
 
 __device__ __forceinline__ int xswizzle(int row) { return (row >> 1) & 7; }
 
-template <int FMT, int STAGES>
+// One step's DMA by one wave into the stage at `base` (the per-lane sources
+// are described at the kernel). The W step stride comes in as `wstep`, a
+// plain argument.
+template <int FMT, int STAGES, int BM>
+__device__ __forceinline__ void issue_step_dma(unsigned char *base, int t, int wave, __amdgpu_buffer_rsrc_t rx,
+                                               __amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs,
+                                               const int (&xsrc)[4], const int (&wsrc)[2], int ssrc, int wstep) {
+  using L = Layout<FMT, STAGES, BM>;
+#pragma unroll
+  for (int k = 0; k < (L::kWDma + 7) / 8; ++k)
+    if (8 * k + wave < L::kWDma)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + L::kXBytes + (8 * k + wave) * 1024), 16,
+                                               wsrc[k], wstep * t, 0, 0);
+  if (L::kMx && wave >= 4 && wave < 4 + L::kSDma)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr *)(base + L::kSOff + (wave - 4) * 256), 2, ssrc, 2 * t, 0,
+                                             0);
+#pragma unroll
+  for (int k = 0; k < L::kXDma; ++k)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr *)(base + (8 * k + wave) * 1024), 16, xsrc[k], 128 * t, 0,
+                                             0);
+}
+
+template <int FMT, int STAGES, int BM>
 __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict__ out,
                                                                const uint16_t *__restrict__ X,
                                                                const uint8_t *__restrict__ Wq,
                                                                const void *__restrict__ scales, int M, int N,
                                                                int K) {
-  using L = Layout<FMT, STAGES>;
+  using L = Layout<FMT, STAGES, BM>;
   __shared__ __attribute__((aligned(1024))) unsigned char lds[L::kLds];
   int tile = blockIdx.x;
   const int tiles = gridDim.x;
   if (tiles % kXcds == 0) tile = (tile % kXcds) * (tiles / kXcds) + tile / kXcds;
-  const int mtiles = (M + kBM - 1) / kBM;
-  const int m0 = (tile % mtiles) * kBM, n0 = (tile / mtiles) * kBN;
-  const int mrows = min(kBM, M - m0), nrows = min(kBN, N - n0);
+  const int mtiles = (M + L::kBM - 1) / L::kBM;
+  const int m0 = (tile % mtiles) * L::kBM, n0 = (tile / mtiles) * L::kBN;
+  const int mrows = min(L::kBM, M - m0), nrows = min(L::kBN, N - n0);
   const int tid = threadIdx.x, lane = tid % L2C_WAVE;
   const int wave = __builtin_amdgcn_readfirstlane(tid / L2C_WAVE);
   const int g = wave >> 2, p = wave & 3;
-  const int wm = p & 1, wn = p >> 1;
+  const int wm = p % L::kWavesM, wn = p / L::kWavesM;
   const int r = lane % 32, h = lane / 32;
   const int xrb = 2 * K;
   const int wrb = L::kMx ? K / 2 : K;
@@ -114,49 +151,42 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
       L::kMx ? l2c::buffer_rsrc(static_cast<const uint8_t *>(scales) + static_cast<size_t>(n0) * srb,
                                 static_cast<uint32_t>(nrows) * srb)
              : rw;
-  const int lrow = 8 * wave + lane / 8;
-  const int lchunk = 16 * ((lane % 8) ^ xswizzle(lrow));
-  int xsrc[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) xsrc[k] = min(64 * k + lrow, mrows - 1) * xrb + lchunk;
-  const int wrow = (64 / L::kLanesPerRow) * wave + lane / L::kLanesPerRow;
-  const int wsrc = min(wrow, nrows - 1) * wrb + 16 * ((lane % L::kLanesPerRow) ^ L::wswizzle(wrow));
-  const int ssrc = min(max(64 * (wave - 4) + lane, 0), nrows - 1) * srb;
 
   // DMA sources (per-lane parts; the step's k offset is scalar). X: block b of
-  // 8 rows (b = 8k + wave), lane i fills row 8b + i / 8, slot i % 8 with chunk
-  // (i % 8) ^ xswizzle(row). W: wave w fills rows (64 / lanes-per-row) w + i /
-  // lanes-per-row, slot i % lanes-per-row. Scales: wave 4 + s fills row 64 s +
-  // i. DMA instructions a wave issues a step: 5, or 4 (MXFP4 waves 6 and 7).
-  auto dma = [&](int stage, int t) __attribute__((always_inline)) {
-    unsigned char *base = lds + stage * L::kStage;
-    if constexpr (L::kMx) {
-      if (wave < 4)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + kXBytes + wave * 1024), 16, wsrc, 32 * t, 0,
-                                                 0);
-      else if (wave < 6)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr *)(base + L::kSOff + (wave - 4) * 256), 2, ssrc, 2 * t,
-                                                 0, 0);
-    } else {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + kXBytes + wave * 1024), 16, wsrc, 64 * t, 0, 0);
-    }
+  // 8 rows (b = 8k + wave, k < BM / 64), lane i fills row 8b + i / 8, slot
+  // i % 8 with chunk (i % 8) ^ xswizzle(row). W: instruction q = 8k + wave
+  // (while q < kWDma) fills rows (64 / lanes-per-row) q + i / lanes-per-row,
+  // slot i % lanes-per-row. MXFP4 scales: wave 4 + s fills row 64 s + i.
+  const int lrow = 8 * wave + lane / 8;
+  const int lchunk = 16 * ((lane % 8) ^ xswizzle(lrow));
+  int xsrc[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr *)(base + (8 * k + wave) * 1024), 16, xsrc[k], 128 * t,
-                                               0, 0);
+  for (int k = 0; k < L::kXDma; ++k) xsrc[k] = min(64 * k + lrow, mrows - 1) * xrb + lchunk;
+  int wsrc[2] = {0, 0};
+#pragma unroll
+  for (int k = 0; k < (L::kWDma + 7) / 8; ++k) {
+    const int wrow = L::kWRowsPerDma * (8 * k + wave) + lane / L::kLanesPerRow;
+    wsrc[k] = min(wrow, nrows - 1) * wrb + 16 * ((lane % L::kLanesPerRow) ^ L::wswizzle(wrow));
+  }
+  const int ssrc = min(max(64 * (wave - 4) + lane, 0), nrows - 1) * srb;
+  const int wstep = L::kWRow;
+  auto dma = [&](int stage, int t) __attribute__((always_inline)) {
+    issue_step_dma<FMT, STAGES, BM>(lds + stage * L::kStage, t, wave, rx, rw, rs, xsrc, wsrc, ssrc, wstep);
   };
   // This wave's DMA of the step after the one just read has landed, its LDS
   // reads are done; then the workgroup barrier. The DMA of the STAGES - 2
-  // newer steps may stay in flight: at most 4 (STAGES - 2) instructions, which
-  // is exact for a wave that issues 4 a step and stricter for one that issues
-  // 5 (one form for every wave: no branch for the compiler to sink the
-  // conversions past).
+  // newer steps may stay in flight (Layout::kWait instructions; one form for
+  // every wave: no branch for the compiler to sink the conversions past).
   auto wait_dma_barrier = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (STAGES == 4)
+    if constexpr (L::kWait == 8)
       asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else
+    else if constexpr (L::kWait == 6)
+      asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (L::kWait == 4)
       asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      static_assert(L::kWait == 8, "no wait form for this layout");
     __builtin_amdgcn_sched_barrier(0);
   };
   auto barrier = [&]() __attribute__((always_inline)) {
@@ -173,8 +203,8 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
   const int a0 = (wm * 128 + r) * 128;
   const int c0 = 16 * ((4 * h + 2 * g) ^ xsw), c1 = 16 * ((4 * h + 2 * g + 1) ^ xsw);
   const int wr0 = wn * 64 + r;
-  const int wb = L::kMx ? kXBytes + wr0 * 32 + 16 * (h ^ L::wswizzle(wr0)) + 8 * g
-                        : kXBytes + wr0 * 64 + 16 * ((2 * h + g) ^ L::wswizzle(wr0));
+  const int wb = L::kMx ? L::kXBytes + wr0 * 32 + 16 * (h ^ L::wswizzle(wr0)) + 8 * g
+                        : L::kXBytes + wr0 * 64 + 16 * ((2 * h + g) ^ L::wswizzle(wr0));
   const int sb = L::kSOff + 4 * wr0;
   u32x4 fa[4][2];
   u32x4 wc[2];
@@ -300,23 +330,28 @@ int l2c_matmul_q_ks(float *out, const uint16_t *X, const uint8_t *Wq, const void
                     int cols, int rows, hipStream_t stream) {
   if (cols % 64 != 0 || (fmt != L2C_Q_MXFP4 && fmt != L2C_Q_FP8)) return hipErrorInvalidValue;
   if (fmt == L2C_Q_MXFP4 && (reinterpret_cast<uintptr_t>(scales) & 1u)) return hipErrorInvalidValue;
-  if (static_cast<long long>(kBM) * cols * 2 > 0x7fffffffLL) return hipErrorInvalidValue;
-  const long long tiles = static_cast<long long>((batch + kBM - 1) / kBM) * ((rows + kBN - 1) / kBN);
+  // MXFP4 takes 256 x 128 tiles, fp8 128 x 256 (same time alone, and its four
+  // 32 KB stages leave LDS for the row kernels beside it in an iteration).
+  const int bm = fmt == L2C_Q_MXFP4 ? 256 : 128, bn = 32768 / bm;
+  // Per-lane byte offsets are ints: a tile's X rows and W rows stay below 2^31.
+  if (static_cast<long long>(bm) * cols * 2 > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (static_cast<long long>(bn) * (fmt == L2C_Q_MXFP4 ? cols / 2 : cols) > 0x7fffffffLL) return hipErrorInvalidValue;
+  const long long tiles = static_cast<long long>((batch + bm - 1) / bm) * ((rows + bn - 1) / bn);
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(tiles)), block(kThreads);
-  // Four stages for both formats (146 KB MXFP4, 160 KB fp8).
+  // Four stages: 146 KB (MXFP4), 128 KB (fp8).
   if (fmt == L2C_Q_MXFP4)
-    hipLaunchKernelGGL((qgemm_ks_kernel<L2C_Q_MXFP4, 4>), grid, block, 0, stream, out, X, Wq, scales, batch, rows,
-                       cols);
+    hipLaunchKernelGGL((qgemm_ks_kernel<L2C_Q_MXFP4, 4, 256>), grid, block, 0, stream, out, X, Wq, scales, batch,
+                       rows, cols);
   else
-    hipLaunchKernelGGL((qgemm_ks_kernel<L2C_Q_FP8, 4>), grid, block, 0, stream, out, X, Wq, scales, batch, rows,
+    hipLaunchKernelGGL((qgemm_ks_kernel<L2C_Q_FP8, 4, 128>), grid, block, 0, stream, out, X, Wq, scales, batch, rows,
                        cols);
   L2C_LAUNCH_CHECK();
   return hipSuccess;
 }
 
 int l2c_qgemm_ks_occupancy(int fmt, int *blocks_per_cu) {
-  const void *fn = fmt == L2C_Q_MXFP4 ? reinterpret_cast<const void *>(qgemm_ks_kernel<L2C_Q_MXFP4, 4>)
-                                      : reinterpret_cast<const void *>(qgemm_ks_kernel<L2C_Q_FP8, 4>);
+  const void *fn = fmt == L2C_Q_MXFP4 ? reinterpret_cast<const void *>(qgemm_ks_kernel<L2C_Q_MXFP4, 4, 256>)
+                                      : reinterpret_cast<const void *>(qgemm_ks_kernel<L2C_Q_FP8, 4, 128>);
   return static_cast<int>(hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, kThreads, 0));
 }
