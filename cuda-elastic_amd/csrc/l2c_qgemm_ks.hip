@@ -46,12 +46,13 @@
 //    Timing probes with work removed: without the DMA 164 / 175 µs, without
 //    the DMA and the fragment reads 149 / 162 µs (the MFMAs alone on these
 //    operands); removing the conversions or the DMA wait changes nothing.
-//    Three stages for fp8 (128 KB, one step for the DMA) measured 213 µs.
-//    fp8 on the 256 x 128 tile needed four 40 KB stages, the CU's whole
-//    LDS, so in the C5 iteration the row kernels could not run beside it.
-//    The 128 x 256 tile gives the same results bit for bit, in the same time
-//    alone (206.5 against 208.5 µs), with 32 KB stages; MXFP4 on it measured
-//    226 against 216 µs and keeps 256 x 128.
+//    fp8 on the 256 x 128 tile took four 40 KB stages, the CU's whole LDS,
+//    so in the C5 iteration the row kernels could not run beside it (three
+//    stages there, one step for the DMA, measured 213 µs). The 128 x 256
+//    tile gives the same results bit for bit with 32 KB stages: alone within
+//    1% (209 against 207 µs on the harness's weights), the graph iteration
+//    252 against 281 µs. MXFP4 on it measured 226 against 216 µs and keeps
+//    256 x 128.
 //  * Every access is in bounds by construction: rows past the operand are
 //    clamped per lane to its last row; those rows are never stored.
 #include "l2c_common.h"
