@@ -92,6 +92,8 @@ int l2c_matmul_bf16_split(float *out, const uint16_t *X, const uint16_t *W, cons
 // called by l2c_matmul_q after its argument checks.
 int l2c_matmul_q_ks(float *out, const uint16_t *X, const uint8_t *Wq, const void *scales, int fmt, int batch,
                     int cols, int rows, hipStream_t stream);
-// Workgroups of that kernel resident per CU (its grid and block are those of
-// the l2c_qgemm.hip kernel: one 512-lane workgroup per 256 x 128 tile).
+// Workgroups of that kernel resident per CU (512-lane workgroups, one per
+// tile: 256 x 128 for MXFP4, 128 x 256 for fp8).
 int l2c_qgemm_ks_occupancy(int fmt, int *blocks_per_cu);
+// Workgroups l2c_matmul_q_ks launches for this shape (its tile depends on fmt).
+long long l2c_qgemm_ks_tiles(int fmt, int batch, int rows);

@@ -412,7 +412,10 @@ int l2c_qgemm_launch_shape(int fmt, int batch, int cols, int rows, int *grid, in
   if (fmt != L2C_Q_MXFP4 && fmt != L2C_Q_FP8) return hipErrorInvalidValue;
   *grid = ((batch + kBM - 1) / kBM) * ((rows + kBN - 1) / kBN);
   *block = kThreads;
-  if (cols % 64 == 0) return l2c_qgemm_ks_occupancy(fmt, blocks_per_cu);
+  if (cols % 64 == 0) {
+    *grid = static_cast<int>(l2c_qgemm_ks_tiles(fmt, batch, rows));
+    return l2c_qgemm_ks_occupancy(fmt, blocks_per_cu);
+  }
   const void *fn = fmt == L2C_Q_MXFP4 ? reinterpret_cast<const void *>(qgemm_kernel<L2C_Q_MXFP4>)
                                       : reinterpret_cast<const void *>(qgemm_kernel<L2C_Q_FP8>);
   return static_cast<int>(hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, kThreads, 0));

@@ -325,19 +325,28 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
 
 }  // namespace
 
+namespace {
+// MXFP4 takes 256 x 128 tiles, fp8 128 x 256 (same time alone, and its four
+// 32 KB stages leave LDS for the row kernels beside it in an iteration).
+int tile_rows(int fmt) { return fmt == L2C_Q_MXFP4 ? 256 : 128; }
+}  // namespace
+
+long long l2c_qgemm_ks_tiles(int fmt, int batch, int rows) {
+  const int bm = tile_rows(fmt), bn = 32768 / bm;
+  return static_cast<long long>((batch + bm - 1) / bm) * ((rows + bn - 1) / bn);
+}
+
 // Called by l2c_matmul_q after its argument checks, for cols % 64 == 0 (and,
 // for MXFP4, scales at an even address: the scale DMAs read 2 bytes).
 int l2c_matmul_q_ks(float *out, const uint16_t *X, const uint8_t *Wq, const void *scales, int fmt, int batch,
                     int cols, int rows, hipStream_t stream) {
   if (cols % 64 != 0 || (fmt != L2C_Q_MXFP4 && fmt != L2C_Q_FP8)) return hipErrorInvalidValue;
   if (fmt == L2C_Q_MXFP4 && (reinterpret_cast<uintptr_t>(scales) & 1u)) return hipErrorInvalidValue;
-  // MXFP4 takes 256 x 128 tiles, fp8 128 x 256 (same time alone, and its four
-  // 32 KB stages leave LDS for the row kernels beside it in an iteration).
-  const int bm = fmt == L2C_Q_MXFP4 ? 256 : 128, bn = 32768 / bm;
+  const int bm = tile_rows(fmt), bn = 32768 / bm;
   // Per-lane byte offsets are ints: a tile's X rows and W rows stay below 2^31.
   if (static_cast<long long>(bm) * cols * 2 > 0x7fffffffLL) return hipErrorInvalidValue;
   if (static_cast<long long>(bn) * (fmt == L2C_Q_MXFP4 ? cols / 2 : cols) > 0x7fffffffLL) return hipErrorInvalidValue;
-  const long long tiles = static_cast<long long>((batch + bm - 1) / bm) * ((rows + bn - 1) / bn);
+  const long long tiles = l2c_qgemm_ks_tiles(fmt, batch, rows);
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(tiles)), block(kThreads);
   // Four stages: 146 KB (MXFP4), 128 KB (fp8).
