@@ -91,11 +91,14 @@ __device__ unsigned mix32(unsigned x) {
   return x ^ (x >> 16);
 }
 
-enum { kCeilF32 = 0, kCeilBf16 = 1, kCeilFp6 = 2 };
+enum { kCeilF32 = 0, kCeilBf16 = 1, kCeilFp6 = 2, kCeilF8F4 = 3, kCeilF8F8 = 4 };
 
 // Each lane holds four operand sets; MFMA (q, t) multiplies set q by set
 // (q + t) % 4 into accumulator t. RANDOM: operand bits from a hash (fp32 and
-// bf16 values with exponents near 1, any 6-bit codes); else a constant.
+// bf16 values with exponents near 1, any 6-bit or 4-bit codes, E4M3 codes
+// with the top exponent bit clear so that none is NaN); else a constant.
+// The scaled types take the operand formats of the block-scaled C5 path:
+// E4M3 x E2M1 (MXFP4 weights) and E4M3 x E4M3 (fp8 weights).
 template <int TYPE, int RANDOM>
 __global__ __launch_bounds__(512) void ceiling_kernel(float *out, int n) {
   const unsigned id = blockIdx.x * 512 + threadIdx.x;
@@ -127,7 +130,7 @@ __global__ __launch_bounds__(512) void ceiling_kernel(float *out, int n) {
         for (int t = 0; t < 8; ++t)
           c[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[q]),
                                                          __builtin_bit_cast(bf16x8, b[(q + t) & 3]), c[t], 0, 0, 0);
-  } else {
+  } else if constexpr (TYPE == kCeilFp6) {
     i32x8 a[4], b[4];
     for (int q = 0; q < 4; ++q)
       for (int v = 0; v < 8; ++v) {
@@ -140,6 +143,25 @@ __global__ __launch_bounds__(512) void ceiling_kernel(float *out, int n) {
 #pragma unroll
         for (int t = 0; t < 8; ++t)
           c[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[q], b[(q + t) & 3], c[t], 3, 3, 0, 127, 0, 127);
+  } else {
+    // A: 32 E4M3 codes a lane (1.0 = 0x38); B: 32 E2M1 codes in 4 VGPRs
+    // (1.0 = 0x2) or 32 E4M3 codes.
+    constexpr bool kFp4 = TYPE == kCeilF8F4;
+    constexpr int kFmtB = kFp4 ? 4 : 0;
+    i32x8 a[4], b[4];
+    for (int q = 0; q < 4; ++q)
+      for (int v = 0; v < 8; ++v) {
+        a[q][v] = static_cast<int>(RANDOM ? mix32(id * 64 + q * 8 + v) & 0xbfbfbfbfu : 0x38383838u);
+        const unsigned rb = mix32(id * 64 + 32 + q * 8 + v);
+        b[q][v] = kFp4 ? (v < 4 ? static_cast<int>(RANDOM ? rb : 0x22222222u) : 0)
+                       : static_cast<int>(RANDOM ? rb & 0xbfbfbfbfu : 0x38383838u);
+      }
+    for (int i = 0; i < n; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          c[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[q], b[(q + t) & 3], c[t], 0, kFmtB, 0, 127, 0, 127);
   }
   float sum = 0.0f;
   for (int t = 0; t < 8; ++t)
@@ -164,7 +186,7 @@ static double ceiling_rate(float *out, int blocks, int n) {
   CHECK(hipEventElapsedTime(&ms, a, b));
   CHECK(hipEventDestroy(a));
   CHECK(hipEventDestroy(b));
-  const double mnk = TYPE == kCeilF32 ? 32.0 * 32 * 2 : TYPE == kCeilBf16 ? 32.0 * 32 * 16 : 32.0 * 32 * 64;
+  const double mnk = TYPE == kCeilF32 ? 32.0 * 32 * 2 : TYPE == kCeilBf16 ? 32.0 * 32 * 16 : 32.0 * 32 * 64;  // scaled: k = 64
   const double flops = 2.0 * mnk * 32.0 * n * reps * blocks * 8.0;  // 32 MFMAs a loop trip, 8 waves a block
   return flops / (ms * 1e9);
 }
@@ -175,14 +197,17 @@ static int run_ceilings() {
   const int blocks = cus;  // one 512-lane block per CU: two waves per SIMD
   float *out = nullptr;
   CHECK(hipMalloc(&out, static_cast<size_t>(blocks) * 512 * 4));
-  const char *names[3] = {"fp32 32x32x2", "bf16 32x32x16", "fp6 (E3M2, scaled) 32x32x64"};
-  const int trips[3] = {400, 2000, 2000};
-  for (int type = 0; type < 3; ++type) {
+  const char *names[5] = {"fp32 32x32x2", "bf16 32x32x16", "fp6 (E3M2, scaled) 32x32x64",
+                          "fp8 x fp4 (E4M3 x E2M1, scaled) 32x32x64", "fp8 x fp8 (E4M3 x E4M3, scaled) 32x32x64"};
+  const int trips[5] = {400, 2000, 2000, 1000, 1000};
+  for (int type = 0; type < 5; ++type) {
     double rc = 0, rr = 0;
     for (int rep = 0; rep < 2; ++rep) {  // the second pass is reported (clocks settled)
       if (type == 0) rc = ceiling_rate<kCeilF32, 0>(out, blocks, trips[0]), rr = ceiling_rate<kCeilF32, 1>(out, blocks, trips[0]);
       if (type == 1) rc = ceiling_rate<kCeilBf16, 0>(out, blocks, trips[1]), rr = ceiling_rate<kCeilBf16, 1>(out, blocks, trips[1]);
       if (type == 2) rc = ceiling_rate<kCeilFp6, 0>(out, blocks, trips[2]), rr = ceiling_rate<kCeilFp6, 1>(out, blocks, trips[2]);
+      if (type == 3) rc = ceiling_rate<kCeilF8F4, 0>(out, blocks, trips[3]), rr = ceiling_rate<kCeilF8F4, 1>(out, blocks, trips[3]);
+      if (type == 4) rc = ceiling_rate<kCeilF8F8, 0>(out, blocks, trips[4]), rr = ceiling_rate<kCeilF8F8, 1>(out, blocks, trips[4]);
     }
     std::printf("ceiling mfma=%s constant_tflops=%.1f random_tflops=%.1f\n", names[type], rc, rr);
   }
