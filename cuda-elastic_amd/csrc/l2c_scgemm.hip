@@ -335,18 +335,18 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_kernel(float *__restr
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  // Ping-pong schedule: the two waves of a SIMD (one per group) run half a
-  // step apart. In its memory phase of step t a wave issues its DMA of step
-  // t + 2 into the stage step t - 1 held, reads its fragments of step t and
-  // waits for its own DMA of step t + 1; in its MFMA phase it runs its 8
-  // MFMAs of step t at raised priority. Group 0's memory phase of step t runs
-  // beside group 1's MFMA phase of step t - 1, and a workgroup barrier ends
-  // every phase. Why three stages suffice: a stage is refilled in the memory
-  // phase after the last one that read it (both groups read step t - 1 before
-  // group 0's memory phase of step t begins), and a step's data has landed
-  // everywhere one memory phase before its first reader, because each wave
-  // waits for its own DMA one step ahead. Group 1 passes one extra barrier at
-  // the start and group 0 one at the end, so both pass the same number.
+  // Ping-pong schedule: the two waves of a SIMD (one per group) run half a step
+  // apart. In its memory phase of step t a wave issues its DMA of step t + 2
+  // into the stage step t - 1 held and reads its fragments of step t (in the
+  // order below), and waits for its own DMA of step t + 1; in its MFMA phase it
+  // runs its 8 MFMAs of step t at raised priority. Group 0's memory phase of
+  // step t runs beside group 1's MFMA phase of step t - 1, and a workgroup
+  // barrier ends every phase. Why three stages suffice: a stage is refilled in
+  // the memory phase after the last one that read it (both groups read step t -
+  // 1 before group 0's memory phase of step t begins), and a step's data has
+  // landed everywhere one memory phase before its first reader, because each
+  // wave waits for its own DMA one step ahead. Group 1 passes one extra barrier
+  // at the start and group 0 one at the end, so both pass the same number.
   const int last = steps - 1;
   dma(0, 0);
   dma(1, min(1, last));
@@ -354,8 +354,17 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_kernel(float *__restr
   if (g == 1) barrier();
   int cur = 0;
   for (int t = 0; t < steps; ++t) {
-    dma(cur == 0 ? kStages - 1 : cur - 1, min(t + 2, last));
-    read(cur);
+    // The order of the DMA issue and the fragment reads: each order measured
+    // 2-2.6% faster for one format (MXFP4 114.1-114.8 against 117.0-117.3 µs
+    // with the DMA first; fp8 125.3-125.9 against 127.9-128.1 µs with the
+    // reads first, at 1024 x 16384 x 8192).
+    if constexpr (G::kMx) {
+      dma(cur == 0 ? kStages - 1 : cur - 1, min(t + 2, last));
+      read(cur);
+    } else {
+      read(cur);
+      dma(cur == 0 ? kStages - 1 : cur - 1, min(t + 2, last));
+    }
     wait_dma_barrier();
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
