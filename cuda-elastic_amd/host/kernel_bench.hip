@@ -6,7 +6,7 @@
 // isolates kernels the same way with ncu).
 //
 //   l2c_kernel_bench OP BATCH SIZE ROWS ITERS   (after >= 100 ms of warm-up launches)
-//   OP: rmsnorm softmax gemv naive fused matmul mxfp4 fp8 copy
+//   OP: rmsnorm softmax gemv naive fused matmul mxfp4 fp8 copy vendor_f32 vendor_bf16
 //       mxfp4s fp8s (the block-scaled product: MXFP8 activation quantizer +
 //       scaled contraction, as l2c_matmul_qs runs them; cvt_mxfp8 the
 //       quantizer alone)
@@ -24,15 +24,29 @@
 // is HBM's rate for W, not a MALL hit's (`gemv` runs back to back, where a W
 // of up to ~256 MB stays in the MALL between launches).
 //
+// `vendor_f32` and `vendor_bf16` time the vendor library's GEMM of the same
+// contraction (hipBLASLt, out[b][r] = sum_k X[b][k] W[r][k] with fp32 or bf16
+// operands, fp32 output and accumulation): the fastest of the library's first
+// eight heuristic choices, picked by a short timing run, then timed like the
+// other ops. They are comparison points only; the product never calls the
+// library. A line `vendor_check` gives the largest difference from this
+// library's own contraction over every output, relative to the largest
+// output magnitude (both apply the bf16 op's alpha of 0.5).
+//
 //   l2c_kernel_bench ceiling
 // measures the matrix-core rate the contractions can reach: register-only
-// loops (no memory traffic) of v_mfma_f32_32x32x2_f32, v_mfma_f32_32x32x16_bf16
-// and the scaled E3M2 v_mfma_scale_f32_32x32x64_f8f6f4, two waves per SIMD,
-// eight independent accumulators, on constant and on random operands. The
+// loops (no memory traffic) of v_mfma_f32_32x32x2_f32, v_mfma_f32_16x16x4_f32, v_mfma_f32_32x32x16_bf16
+// and the scaled v_mfma_scale_f32_32x32x64_f8f6f4 (E3M2 x E3M2, E4M3 x E2M1,
+// E4M3 x E4M3), two waves per SIMD,
+// eight independent accumulators, on constant and on random operands, and on
+// random operands with one wave per SIMD (256-lane blocks). The
 // random-operand rate is the one real data meets (the matrix cores' power
 // draw depends on the operand bits).
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -76,9 +90,110 @@ __global__ void fill_kernel(float *p, size_t n, unsigned seed, float scale) {
   }
 }
 
+#define BLT(call)                                                                      \
+  do {                                                                                 \
+    const hipblasStatus_t e__ = (call);                                                \
+    if (e__ != HIPBLAS_STATUS_SUCCESS) {                                               \
+      std::fprintf(stderr, "%s failed: status %d\n", #call, static_cast<int>(e__));    \
+      std::exit(1);                                                                    \
+    }                                                                                  \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Vendor GEMM (comparison only). Column-major views of the row-major operands:
+// W (R x K) is K x R and taken transposed, X (B x K) is K x B, out (B x R) is
+// R x B.
+struct VendorGemm {
+  hipblasLtHandle_t handle = nullptr;
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  void *workspace = nullptr;
+  size_t workspace_bytes = 0;
+  float alpha = 1.0f, beta = 0.0f;
+
+  void run(float *out, const void *W, const void *X, hipStream_t s) const {
+    BLT(hipblasLtMatmul(handle, desc, &alpha, W, la, X, lb, &beta, out, lc, out, lc, &algo, workspace,
+                        workspace_bytes, s));
+  }
+};
+
+static VendorGemm vendor_setup(bool bf16, int B, int K, int R, float *out, const void *W, const void *X,
+                               hipStream_t s) {
+  VendorGemm v;
+  const hipDataType in = bf16 ? HIP_R_16BF : HIP_R_32F;
+  BLT(hipblasLtCreate(&v.handle));
+  BLT(hipblasLtMatmulDescCreate(&v.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
+  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  BLT(hipblasLtMatmulDescSetAttribute(v.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta));
+  BLT(hipblasLtMatmulDescSetAttribute(v.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb));
+  BLT(hipblasLtMatrixLayoutCreate(&v.la, in, K, R, K));
+  BLT(hipblasLtMatrixLayoutCreate(&v.lb, in, K, B, K));
+  BLT(hipblasLtMatrixLayoutCreate(&v.lc, HIP_R_32F, R, B, R));
+  hipblasLtMatmulPreference_t pref = nullptr;
+  BLT(hipblasLtMatmulPreferenceCreate(&pref));
+  const uint64_t max_ws = uint64_t(256) << 20;
+  BLT(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &max_ws,
+                                            sizeof max_ws));
+  hipblasLtMatmulHeuristicResult_t res[8];
+  int n = 0;
+  BLT(hipblasLtMatmulAlgoGetHeuristic(v.handle, v.desc, v.la, v.lb, v.lc, v.lc, pref, 8, res, &n));
+  BLT(hipblasLtMatmulPreferenceDestroy(pref));
+  if (n < 1) {
+    std::fprintf(stderr, "hipBLASLt offers no algorithm for this GEMM\n");
+    std::exit(1);
+  }
+  size_t most = 0;
+  for (int i = 0; i < n; ++i) most = std::max(most, res[i].workspaceSize);
+  if (most > 0) CHECK(hipMalloc(&v.workspace, most));
+  hipEvent_t a, b;
+  CHECK(hipEventCreate(&a));
+  CHECK(hipEventCreate(&b));
+  float best = 0.0f;
+  int pick = -1;
+  for (int i = 0; i < n; ++i) {
+    if (res[i].state != HIPBLAS_STATUS_SUCCESS) continue;
+    v.algo = res[i].algo;
+    v.workspace_bytes = res[i].workspaceSize;
+    for (int w = 0; w < 5; ++w) v.run(out, W, X, s);
+    CHECK(hipEventRecord(a, s));
+    for (int r = 0; r < 10; ++r) v.run(out, W, X, s);
+    CHECK(hipEventRecord(b, s));
+    CHECK(hipEventSynchronize(b));
+    float ms = 0.0f;
+    CHECK(hipEventElapsedTime(&ms, a, b));
+    std::printf("vendor_candidate=%d us=%.3f workspace=%zu\n", i, 100.0 * ms, res[i].workspaceSize);
+    if (pick < 0 || ms < best) best = ms, pick = i;
+  }
+  if (pick < 0) {
+    std::fprintf(stderr, "hipBLASLt returned no usable algorithm\n");
+    std::exit(1);
+  }
+  v.algo = res[pick].algo;
+  v.workspace_bytes = res[pick].workspaceSize;
+  CHECK(hipEventDestroy(a));
+  CHECK(hipEventDestroy(b));
+  std::printf("vendor_pick=%d of %d\n", pick, n);
+  return v;
+}
+
+// Largest |a - b| over n device outputs, relative to the largest |b|.
+static double max_rel_diff(const float *a, const float *b, size_t n) {
+  std::vector<float> ha(n), hb(n);
+  CHECK(hipMemcpy(ha.data(), a, n * 4, hipMemcpyDeviceToHost));
+  CHECK(hipMemcpy(hb.data(), b, n * 4, hipMemcpyDeviceToHost));
+  double diff = 0.0, big = 0.0;
+  for (size_t i = 0; i < n; ++i) {
+    diff = std::max(diff, static_cast<double>(std::fabs(ha[i] - hb[i])));
+    big = std::max(big, static_cast<double>(std::fabs(hb[i])));
+  }
+  return big > 0.0 ? diff / big : diff;
+}
+
 // ---------------------------------------------------------------------------
 // Matrix-core ceilings.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
@@ -91,7 +206,7 @@ __device__ unsigned mix32(unsigned x) {
   return x ^ (x >> 16);
 }
 
-enum { kCeilF32 = 0, kCeilBf16 = 1, kCeilFp6 = 2, kCeilF8F4 = 3, kCeilF8F8 = 4 };
+enum { kCeilF32 = 0, kCeilBf16 = 1, kCeilFp6 = 2, kCeilF8F4 = 3, kCeilF8F8 = 4, kCeilF32x16 = 5 };
 
 // Each lane holds four operand sets; MFMA (q, t) multiplies set q by set
 // (q + t) % 4 into accumulator t. RANDOM: operand bits from a hash (fp32 and
@@ -105,7 +220,21 @@ __global__ __launch_bounds__(512) void ceiling_kernel(float *out, int n) {
   f32x16 c[8];
   for (int t = 0; t < 8; ++t)
     for (int v = 0; v < 16; ++v) c[t][v] = 0.0f;
-  if constexpr (TYPE == kCeilF32) {
+  if constexpr (TYPE == kCeilF32x16) {
+    float a[4], b[4];
+    for (int q = 0; q < 4; ++q) {
+      a[q] = RANDOM ? __uint_as_float((mix32(id * 8 + q) & 0x807fffffu) | 0x3f000000u) : 1.0f;
+      b[q] = RANDOM ? __uint_as_float((mix32(id * 8 + q + 4) & 0x807fffffu) | 0x3f000000u) : 1.0f;
+    }
+    f32x4 d[8];
+    for (int t = 0; t < 8; ++t) d[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < n; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) d[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[q], b[(q + t) & 3], d[t], 0, 0, 0);
+    for (int t = 0; t < 8; ++t) c[t][0] = d[t][0] + d[t][1] + d[t][2] + d[t][3];
+  } else if constexpr (TYPE == kCeilF32) {
     float a[4], b[4];
     for (int q = 0; q < 4; ++q) {
       a[q] = RANDOM ? __uint_as_float((mix32(id * 8 + q) & 0x807fffffu) | 0x3f000000u) : 1.0f;
@@ -169,9 +298,12 @@ __global__ __launch_bounds__(512) void ceiling_kernel(float *out, int n) {
   out[id] = sum;
 }
 
+// threads = 512: one block per CU is two waves per SIMD; 256: one wave per
+// SIMD, the matrix core fed by a single wave.
 template <int TYPE, int RANDOM>
-static double ceiling_rate(float *out, int blocks, int n) {
-  for (int w = 0; w < 3; ++w) hipLaunchKernelGGL((ceiling_kernel<TYPE, RANDOM>), dim3(blocks), dim3(512), 0, nullptr, out, n);
+static double ceiling_rate(float *out, int blocks, int n, int threads) {
+  for (int w = 0; w < 3; ++w)
+    hipLaunchKernelGGL((ceiling_kernel<TYPE, RANDOM>), dim3(blocks), dim3(threads), 0, nullptr, out, n);
   CHECK(hipGetLastError());
   hipEvent_t a, b;
   CHECK(hipEventCreate(&a));
@@ -179,38 +311,46 @@ static double ceiling_rate(float *out, int blocks, int n) {
   const int reps = 5;
   CHECK(hipEventRecord(a));
   for (int r = 0; r < reps; ++r)
-    hipLaunchKernelGGL((ceiling_kernel<TYPE, RANDOM>), dim3(blocks), dim3(512), 0, nullptr, out, n);
+    hipLaunchKernelGGL((ceiling_kernel<TYPE, RANDOM>), dim3(blocks), dim3(threads), 0, nullptr, out, n);
   CHECK(hipEventRecord(b));
   CHECK(hipEventSynchronize(b));
   float ms = 0.0f;
   CHECK(hipEventElapsedTime(&ms, a, b));
   CHECK(hipEventDestroy(a));
   CHECK(hipEventDestroy(b));
-  const double mnk = TYPE == kCeilF32 ? 32.0 * 32 * 2 : TYPE == kCeilBf16 ? 32.0 * 32 * 16 : 32.0 * 32 * 64;  // scaled: k = 64
-  const double flops = 2.0 * mnk * 32.0 * n * reps * blocks * 8.0;  // 32 MFMAs a loop trip, 8 waves a block
+  const double mnk = TYPE == kCeilF32     ? 32.0 * 32 * 2
+                     : TYPE == kCeilF32x16 ? 16.0 * 16 * 4
+                     : TYPE == kCeilBf16   ? 32.0 * 32 * 16
+                                           : 32.0 * 32 * 64;  // scaled: k = 64
+  const double waves = threads / 64.0;
+  const double flops = 2.0 * mnk * 32.0 * n * reps * blocks * waves;  // 32 MFMAs a loop trip
   return flops / (ms * 1e9);
+}
+
+template <int TYPE>
+static void ceiling_line(const char *name, float *out, int blocks, int trips) {
+  double rc = 0, rr = 0, r1 = 0;
+  for (int rep = 0; rep < 2; ++rep) {  // the second pass is reported (clocks settled)
+    rc = ceiling_rate<TYPE, 0>(out, blocks, trips, 512);
+    rr = ceiling_rate<TYPE, 1>(out, blocks, trips, 512);
+    r1 = ceiling_rate<TYPE, 1>(out, blocks, trips, 256);
+  }
+  std::printf("ceiling mfma=%s constant_tflops=%.1f random_tflops=%.1f random_one_wave_tflops=%.1f\n", name, rc, rr,
+              r1);
 }
 
 static int run_ceilings() {
   int cus = 0;
   CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
-  const int blocks = cus;  // one 512-lane block per CU: two waves per SIMD
+  const int blocks = cus;  // one block per CU
   float *out = nullptr;
   CHECK(hipMalloc(&out, static_cast<size_t>(blocks) * 512 * 4));
-  const char *names[5] = {"fp32 32x32x2", "bf16 32x32x16", "fp6 (E3M2, scaled) 32x32x64",
-                          "fp8 x fp4 (E4M3 x E2M1, scaled) 32x32x64", "fp8 x fp8 (E4M3 x E4M3, scaled) 32x32x64"};
-  const int trips[5] = {400, 2000, 2000, 1000, 1000};
-  for (int type = 0; type < 5; ++type) {
-    double rc = 0, rr = 0;
-    for (int rep = 0; rep < 2; ++rep) {  // the second pass is reported (clocks settled)
-      if (type == 0) rc = ceiling_rate<kCeilF32, 0>(out, blocks, trips[0]), rr = ceiling_rate<kCeilF32, 1>(out, blocks, trips[0]);
-      if (type == 1) rc = ceiling_rate<kCeilBf16, 0>(out, blocks, trips[1]), rr = ceiling_rate<kCeilBf16, 1>(out, blocks, trips[1]);
-      if (type == 2) rc = ceiling_rate<kCeilFp6, 0>(out, blocks, trips[2]), rr = ceiling_rate<kCeilFp6, 1>(out, blocks, trips[2]);
-      if (type == 3) rc = ceiling_rate<kCeilF8F4, 0>(out, blocks, trips[3]), rr = ceiling_rate<kCeilF8F4, 1>(out, blocks, trips[3]);
-      if (type == 4) rc = ceiling_rate<kCeilF8F8, 0>(out, blocks, trips[4]), rr = ceiling_rate<kCeilF8F8, 1>(out, blocks, trips[4]);
-    }
-    std::printf("ceiling mfma=%s constant_tflops=%.1f random_tflops=%.1f\n", names[type], rc, rr);
-  }
+  ceiling_line<kCeilF32>("fp32 32x32x2", out, blocks, 400);
+  ceiling_line<kCeilBf16>("bf16 32x32x16", out, blocks, 2000);
+  ceiling_line<kCeilFp6>("fp6 (E3M2, scaled) 32x32x64", out, blocks, 2000);
+  ceiling_line<kCeilF8F4>("fp8 x fp4 (E4M3 x E2M1, scaled) 32x32x64", out, blocks, 1000);
+  ceiling_line<kCeilF8F8>("fp8 x fp8 (E4M3 x E4M3, scaled) 32x32x64", out, blocks, 1000);
+  ceiling_line<kCeilF32x16>("fp32 16x16x4", out, blocks, 800);
   CHECK(hipFree(out));
   return 0;
 }
@@ -250,7 +390,9 @@ int main(int argc, char **argv) {
   uint8_t *codes = nullptr, *sc8 = nullptr, *xq = nullptr, *xs = nullptr, *ws = nullptr;
   size_t ws_bytes = 0;
   float *sc32 = nullptr, *alpha = nullptr, *partials = nullptr, *tscales = nullptr;
-  if (op == "bf16" || op == "mxfp6" || op == "cvt_bf16" || op == "cvt_mxfp6" || op == "cvt_nvfp4") {
+  const bool vendor = op == "vendor_f32" || op == "vendor_bf16";
+  if (op == "bf16" || op == "vendor_bf16" || op == "mxfp6" || op == "cvt_bf16" || op == "cvt_mxfp6" ||
+      op == "cvt_nvfp4") {
     if (S % 128 != 0) {
       std::fprintf(stderr, "lowprec ops need SIZE %% 128 == 0\n");
       return 2;
@@ -263,7 +405,7 @@ int main(int argc, char **argv) {
     CHECK(hipMalloc(&partials, L2C_NVFP4_PARTIALS * 4));
     const float one = 0.5f;
     CHECK(hipMemcpy(alpha, &one, 4, hipMemcpyHostToDevice));
-    if (op == "bf16") {
+    if (op == "bf16" || op == "vendor_bf16") {
       CHECK(hipMalloc(&wb, mat * 2));
       L2C(l2c_to_bf16_x4(xb, x, static_cast<long long>(vec), nullptr));
       L2C(l2c_to_bf16_x4(wb, m, static_cast<long long>(mat), nullptr));
@@ -306,6 +448,13 @@ int main(int argc, char **argv) {
 
   hipStream_t s;
   CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  VendorGemm vg;
+  if (vendor) {
+    const bool bf = op == "vendor_bf16";
+    vg = vendor_setup(bf, B, S, R, prod, bf ? static_cast<const void *>(wb) : m,
+                      bf ? static_cast<const void *>(xb) : x, s);
+    if (bf) vg.alpha = 0.5f;  // the bf16 op's alpha
+  }
   double bytes = 0, flops = 0;
   auto launch = [&]() {
     if (op == "rmsnorm") {
@@ -358,6 +507,14 @@ int main(int argc, char **argv) {
       L2C(l2c_nvfp4_tensor_scales(tscales, alpha, tscales + 1, x, static_cast<long long>(vec), partials, s));
       L2C(l2c_quantize_nvfp4(xq, xs, xb, x, tscales, B, S, s));
       bytes = vec * (4.0 + 4.0 + 0.5 + 1.0 / 16 + 2.0);
+    } else if (op == "vendor_f32") {
+      vg.run(prod, m, x, s);
+      bytes = (vec + mat + static_cast<double>(B) * R) * 4;
+      flops = 2.0 * B * static_cast<double>(mat);
+    } else if (op == "vendor_bf16") {
+      vg.run(prod, wb, xb, s);
+      bytes = (vec + static_cast<double>(mat)) * 2 + static_cast<double>(B) * R * 4;
+      flops = 2.0 * B * static_cast<double>(mat);
     } else if (op == "copy") {
       hipLaunchKernelGGL(copy_kernel, dim3(4096), dim3(256), 0, s, reinterpret_cast<float4 *>(o1),
                          reinterpret_cast<const float4 *>(x), vec / 4);
@@ -414,6 +571,16 @@ int main(int argc, char **argv) {
   float ms = 0;
   CHECK(hipEventElapsedTime(&ms, t0, t1));
   const double us = 1000.0 * ms / iters;
+  if (vendor) {
+    // The same contraction by this library, for the vendor_check line.
+    float *ref = nullptr;
+    CHECK(hipMalloc(&ref, static_cast<size_t>(B) * R * 4));
+    if (op == "vendor_f32") L2C(l2c_matmul(ref, x, m, B, S, R, s));
+    else L2C(l2c_matmul_bf16(ref, xb, wb, alpha, B, S, R, s));
+    CHECK(hipStreamSynchronize(s));
+    std::printf("vendor_check max_rel_diff=%.3e\n", max_rel_diff(prod, ref, static_cast<size_t>(B) * R));
+    CHECK(hipFree(ref));
+  }
   std::printf("op=%s batch=%d size=%d rows=%d iters=%d warmup=%d avg_us=%.3f bytes=%.0f gbps=%.1f tflops=%.3f\n",
               op.c_str(), B, S, R, iters, warm, us, bytes, bytes / (us * 1e3), flops / (us * 1e6));
   return 0;
