@@ -196,7 +196,10 @@ __global__ __launch_bounds__(kThreads, 1) void bf16_gemm_kernel(float *__restric
         for (int v = 0; v < 16; ++v) {
           const int m = wm * 128 + 32 * i + 8 * (v / 4) + 4 * h + v % 4;
           const float sum = acc[i][j][v] + exchange[((p * 8 + i * 2 + j) * 16 + v) * L2C_WAVE + lane];
-          if (m < mrows && n < nrows) out[static_cast<size_t>(m0 + m) * N + n0 + n] = sum * a;
+          // Nontemporal stores: 218.2-218.3 against 218.9-219.2 µs with
+          // ordinary ones at 1024 x 16384 x 8192, one box.
+          if (m < mrows && n < nrows)
+            __builtin_nontemporal_store(sum * a, &out[static_cast<size_t>(m0 + m) * N + n0 + n]);
         }
     }
   }

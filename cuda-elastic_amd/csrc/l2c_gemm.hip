@@ -102,7 +102,9 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[kFragM][kFragN]) {
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 }
 
-// Lanes 0-31 and 32-63 each write 32 consecutive floats of an output row.
+// Lanes 0-31 and 32-63 each write 32 consecutive floats of an output row,
+// with nontemporal stores (written once; 1848.7-1849.6 against 1850.8-1851.2
+// µs with ordinary stores at 1024 x 16384 x 8192, one box).
 __device__ __forceinline__ void store_tile(float *out, const f32x16 (&acc)[kFragM][kFragN], int m0,
                                            int n0, int M, int N, int wm, int wn, int lane) {
 #pragma unroll
@@ -113,7 +115,7 @@ __device__ __forceinline__ void store_tile(float *out, const f32x16 (&acc)[kFrag
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int m = m0 + wm * kWaveM + i * 32 + 8 * (v / 4) + 4 * (lane / 32) + v % 4;
-        if (m < M && n < N) out[static_cast<size_t>(m) * N + n] = acc[i][j][v];
+        if (m < M && n < N) __builtin_nontemporal_store(acc[i][j][v], &out[static_cast<size_t>(m) * N + n]);
       }
     }
   }

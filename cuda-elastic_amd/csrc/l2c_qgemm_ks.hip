@@ -320,7 +320,12 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_ks_kernel(float *__restrict
         for (int v = 0; v < 16; ++v) {
           const int m = wm * 128 + 32 * i + 8 * (v / 4) + 4 * h + v % 4;
           const float sum = acc[i][j][v] + exchange[((p * 8 + i * 2 + j) * 16 + v) * L2C_WAVE + lane];
-          if (m < mrows && n < nrows) out[static_cast<size_t>(m0 + m) * N + n0 + n] = sum * rscale;
+          // Nontemporal: the tile's outputs are written once, at the end of
+          // the launch, when every CU stores at once (fp8 198.2-198.6 against
+          // 199.9-200.7 µs with ordinary stores, MXFP4 200.8-201.1 against
+          // 202.2-202.5, at 1024 x 16384 x 8192 on one box).
+          if (m < mrows && n < nrows)
+            __builtin_nontemporal_store(sum * rscale, &out[static_cast<size_t>(m0 + m) * N + n0 + n]);
         }
     }
   }

@@ -415,7 +415,11 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_kernel(float *__restr
         for (int v = 0; v < 16; ++v) {
           const int m = wm * 128 + 32 * i + 8 * (v / 4) + 4 * h + v % 4;
           const float sum = acc[i][j][v] + exchange[((p * 8 + i * 2 + j) * 16 + v) * L2C_WAVE + lane];
-          if (m < mrows && n < nrows) out[static_cast<size_t>(m0 + m) * N + n0 + n] = sum * rscale;
+          // Nontemporal stores: MXFP4 112.5-112.8 against 114.1-114.3 µs with
+          // ordinary ones, fp8 123.2-123.7 against 125.3-125.5 (the product,
+          // quantizer included, at 1024 x 16384 x 8192 on one box).
+          if (m < mrows && n < nrows)
+            __builtin_nontemporal_store(sum * rscale, &out[static_cast<size_t>(m0 + m) * N + n0 + n]);
         }
     }
   }
