@@ -266,6 +266,7 @@ def main():
             ("c4_gemv_graph_nocopy", cfg("graph", 200, B, S, R, "nocopy", "coalesced")),
             ("c4_gemv_direct_nocopy", cfg("direct", 200, B, S, R, "nocopy", "coalesced")),
             ("c4_fused_graph_nocopy", cfg("graph", 200, B, S, R, "nocopy", "fused")),
+            ("c4_fused_direct_nocopy", cfg("direct", 200, B, S, R, "nocopy", "fused")),
             ("c2_gemv_graph_nocopy", cfg("graph", 1000, 1, 4096, 11008, "nocopy", "coalesced", warm=50)),
             ("c2_gemv_direct_nocopy", cfg("direct", 1000, 1, 4096, 11008, "nocopy", "coalesced", warm=50)),
             ("c2_fused_graph_nocopy", cfg("graph", 1000, 1, 4096, 11008, "nocopy", "fused", warm=50)),

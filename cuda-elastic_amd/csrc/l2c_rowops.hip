@@ -29,6 +29,13 @@
 //  * The naive product keeps the reference's one-lane-per-row structure and
 //    its sequential column order (one fused multiply-add per column), so its
 //    result is bit-reproducible by a CPU fmaf chain.
+//  * The fused iteration is one grid of the standalone kernels' workgroups:
+//    rmsnorm and softmax rows in the row kernels' configuration, then matrix
+//    rows one per wavefront with the standalone product's load choice, so its
+//    outputs equal the three separate launches' bit for bit. At 1024 x 16384
+//    x 8192 (one box, alternating runs) it took 123.3 against 135.3 us for
+//    the earlier form that ran every part at 256 lanes (a whole workgroup per
+//    matrix row, rows at 16 float4 a lane).
 #include "l2c_rows.h"
 #include "../../include/l2c.h"
 
@@ -38,9 +45,6 @@ using l2c::Row;
 
 constexpr int kMaxRowThreads = 1024;
 constexpr int kGenericThreads = 256;
-// The fused kernel holds a matrix row and streams x beside it, so it is
-// limited to 256 lanes per row (<= 16384 floats in registers).
-constexpr int kFusedThreads = 256;
 
 // ---------------------------------------------------------------------------
 // Kernels. V == 0 selects the two-pass generic path; MAXT is the launch
@@ -74,16 +78,17 @@ __global__ __launch_bounds__(MAXT) void softmax_kernel(float *out, const float *
   }
 }
 
-// One launch for a whole llama2c iteration. Block b handles:
+// One launch for a whole llama2c iteration, in workgroups of the row
+// kernels' size T. Block b handles:
 //   b < 2*pairs           rmsnorm row b/2 (even b) or softmax row b/2 (odd b)
 //   then                  the remaining rmsnorm rows, then remaining softmax rows
-//   then                  matrix-vector rows
+//   then                  T / 64 matrix rows, one per wavefront
 // so the short matrix-vector blocks fill the tail of the launch.
-template <int V, bool VEC, bool EXACT, int MAXT>
+template <int V, bool VEC, bool EXACT, int MAXT, bool NT>
 __global__ __launch_bounds__(MAXT) void fused_kernel(
     float *normalized, const float *input, const float *weight, float *softmax,
     const float *logits, float *product, const float *matrix, int size, int rms_rows,
-    int softmax_rows, float eps) {
+    int softmax_rows, int matmul_rows, float eps) {
   __shared__ float slots[32];
   int item = blockIdx.x;
   const int pairs = min(rms_rows, softmax_rows);
@@ -99,24 +104,25 @@ __global__ __launch_bounds__(MAXT) void fused_kernel(
     row = pairs + item;
   } else {
     kind = 2;
-    row = item - (softmax_rows - pairs);
+    row = (item - (softmax_rows - pairs)) * (blockDim.x / L2C_WAVE) + threadIdx.x / L2C_WAVE;
+  }
+  if (kind == 2) {
+    if (row < matmul_rows)
+      l2c::matvec_wave_row<VEC, NT>(product, input, matrix, size, row, threadIdx.x % L2C_WAVE);
+    return;
   }
   const size_t off = static_cast<size_t>(row) * size;
   if constexpr (V == 0) {
     if (kind == 0) l2c::rmsnorm_row_generic(normalized + off, input + off, weight, size, eps, slots);
-    else if (kind == 1) l2c::softmax_row_generic(softmax + off, logits + off, size, slots);
-    else l2c::matvec_row_block_generic(product + row, matrix + off, input, size, slots);
+    else l2c::softmax_row_generic(softmax + off, logits + off, size, slots);
   } else {
+    Row<V, VEC, EXACT> r;
     if (kind == 0) {
-      Row<V, VEC, EXACT> r;
       r.load(input + off, size, 0.0f);
       l2c::rmsnorm_apply(r, normalized + off, weight, size, eps, slots);
-    } else if (kind == 1) {
-      Row<V, VEC, EXACT> r;
+    } else {
       r.load(logits + off, size, -FLT_MAX);
       l2c::softmax_apply_1r(r, softmax + off, size, slots);
-    } else {
-      l2c::matvec_row_block<V, VEC, EXACT>(product + row, matrix + off, input, size, slots);
     }
   }
 }
@@ -139,51 +145,15 @@ constexpr int kMatvecWaves = 4;
 template <bool VEC, bool NT>
 __global__ __launch_bounds__(kMatvecWaves * L2C_WAVE) void matvec_wave_kernel(
     float *out, const float *x, const float *W, int cols, int rows) {
-  const int lane = threadIdx.x % L2C_WAVE;
   const int row = blockIdx.x * kMatvecWaves + threadIdx.x / L2C_WAVE;
-  if (row >= rows) return;
-  const float *w = W + static_cast<size_t>(row) * cols;
-  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-  if constexpr (VEC) {
-    const float4 *w4 = reinterpret_cast<const float4 *>(w);
-    const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    const int cols4 = cols >> 2;
-    int c = lane;
-    // Four independent 1 KiB wave loads in flight per step.
-    for (; c + 3 * L2C_WAVE < cols4; c += 4 * L2C_WAVE) {
-      const float4 m0 = NT ? l2c::ld4_stream(w4 + c) : w4[c];
-      const float4 m1 = NT ? l2c::ld4_stream(w4 + c + L2C_WAVE) : w4[c + L2C_WAVE];
-      const float4 m2 = NT ? l2c::ld4_stream(w4 + c + 2 * L2C_WAVE) : w4[c + 2 * L2C_WAVE];
-      const float4 m3 = NT ? l2c::ld4_stream(w4 + c + 3 * L2C_WAVE) : w4[c + 3 * L2C_WAVE];
-      const float4 v0 = x4[c], v1 = x4[c + L2C_WAVE];
-      const float4 v2 = x4[c + 2 * L2C_WAVE], v3 = x4[c + 3 * L2C_WAVE];
-      a0 = fmaf(m0.x, v0.x, a0); a0 = fmaf(m0.y, v0.y, a0);
-      a0 = fmaf(m0.z, v0.z, a0); a0 = fmaf(m0.w, v0.w, a0);
-      a1 = fmaf(m1.x, v1.x, a1); a1 = fmaf(m1.y, v1.y, a1);
-      a1 = fmaf(m1.z, v1.z, a1); a1 = fmaf(m1.w, v1.w, a1);
-      a2 = fmaf(m2.x, v2.x, a2); a2 = fmaf(m2.y, v2.y, a2);
-      a2 = fmaf(m2.z, v2.z, a2); a2 = fmaf(m2.w, v2.w, a2);
-      a3 = fmaf(m3.x, v3.x, a3); a3 = fmaf(m3.y, v3.y, a3);
-      a3 = fmaf(m3.z, v3.z, a3); a3 = fmaf(m3.w, v3.w, a3);
-    }
-    for (; c < cols4; c += L2C_WAVE) {
-      const float4 m0 = l2c::ld4_stream(w4 + c);
-      const float4 v0 = x4[c];
-      a0 = fmaf(m0.x, v0.x, a0); a0 = fmaf(m0.y, v0.y, a0);
-      a0 = fmaf(m0.z, v0.z, a0); a0 = fmaf(m0.w, v0.w, a0);
-    }
-  } else {
-    int c = lane;
-    for (; c + 3 * L2C_WAVE < cols; c += 4 * L2C_WAVE) {
-      a0 = fmaf(__builtin_nontemporal_load(w + c), x[c], a0);
-      a1 = fmaf(__builtin_nontemporal_load(w + c + L2C_WAVE), x[c + L2C_WAVE], a1);
-      a2 = fmaf(__builtin_nontemporal_load(w + c + 2 * L2C_WAVE), x[c + 2 * L2C_WAVE], a2);
-      a3 = fmaf(__builtin_nontemporal_load(w + c + 3 * L2C_WAVE), x[c + 3 * L2C_WAVE], a3);
-    }
-    for (; c < cols; c += L2C_WAVE) a0 = fmaf(__builtin_nontemporal_load(w + c), x[c], a0);
-  }
-  const float acc = l2c::wave_sum((a0 + a1) + (a2 + a3));
-  if (lane == 0) out[row] = acc;
+  if (row < rows) l2c::matvec_wave_row<VEC, NT>(out, x, W, cols, row, threadIdx.x % L2C_WAVE);
+}
+
+// Nontemporal matrix loads, except for a matrix of 128-256 MiB, which the
+// 256 MB MALL keeps between launches when it is read with ordinary loads.
+bool matvec_nontemporal(int cols, int rows) {
+  const unsigned long long w_bytes = 4ULL * static_cast<unsigned long long>(rows) * cols;
+  return !(w_bytes > (128ULL << 20) && w_bytes <= (256ULL << 20));
 }
 
 // ---------------------------------------------------------------------------
@@ -218,7 +188,7 @@ RowConfig choose_row_config(int size, int max_threads = kMaxRowThreads) {
 using RmsFn = void (*)(float *, const float *, const float *, int, float);
 using SoftFn = void (*)(float *, const float *, int);
 using FusedFn = void (*)(float *, const float *, const float *, float *, const float *, float *,
-                         const float *, int, int, int, float);
+                         const float *, int, int, int, int, float);
 
 // Kernel instance for (V, vector path, exact, launch bound).
 template <int V, int MAXT>
@@ -230,10 +200,6 @@ struct Pick {
   static SoftFn soft(bool vec, bool exact) {
     if (!vec) return softmax_kernel<V, false, false, MAXT>;
     return exact ? softmax_kernel<V, true, true, MAXT> : softmax_kernel<V, true, false, MAXT>;
-  }
-  static FusedFn fused(bool vec, bool exact) {
-    if (!vec) return fused_kernel<V, false, false, MAXT>;
-    return exact ? fused_kernel<V, true, true, MAXT> : fused_kernel<V, true, false, MAXT>;
   }
 };
 
@@ -261,15 +227,30 @@ SoftFn soft_for(int v, bool vec, bool exact) {
   }
 }
 
-FusedFn fused_for(int v, bool vec, bool exact) {
-  switch (v) {
-    case 1: return Pick<1, kFusedThreads>::fused(vec, exact);
-    case 2: return Pick<2, kFusedThreads>::fused(vec, exact);
-    case 4: return Pick<4, kFusedThreads>::fused(vec, exact);
-    case 8: return Pick<8, kFusedThreads>::fused(vec, exact);
-    case 16: return Pick<16, kFusedThreads>::fused(vec, exact);
-    default: return fused_kernel<0, false, false, kFusedThreads>;
+// Fused kernel instances for the (lanes, V) pairs choose_row_config returns:
+// up to 256 lanes with V <= 8, 512 lanes with V = 8, 1024 lanes with V = 8 or
+// 16, and the generic path (V = 0) at 256 lanes.
+template <int V, int MAXT, bool NT>
+FusedFn fused_pick(bool vec, bool exact) {
+  if (!vec) return fused_kernel<V, false, false, MAXT, NT>;
+  return exact ? fused_kernel<V, true, true, MAXT, NT> : fused_kernel<V, true, false, MAXT, NT>;
+}
+
+template <bool NT>
+FusedFn fused_for(const RowConfig &c, bool vec) {
+  const bool exact = vec && c.exact;
+  if (c.v == 0)
+    return vec ? fused_kernel<0, true, false, kGenericThreads, NT> : fused_kernel<0, false, false, kGenericThreads, NT>;
+  if (c.threads <= 256) {
+    switch (c.v) {
+      case 1: return fused_pick<1, 256, NT>(vec, exact);
+      case 2: return fused_pick<2, 256, NT>(vec, exact);
+      case 4: return fused_pick<4, 256, NT>(vec, exact);
+      default: return fused_pick<8, 256, NT>(vec, exact);
+    }
   }
+  if (c.threads <= 512) return fused_pick<8, 512, NT>(vec, exact);
+  return c.v == 8 ? fused_pick<8, kMaxRowThreads, NT>(vec, exact) : fused_pick<16, kMaxRowThreads, NT>(vec, exact);
 }
 
 RmsFn rms_fn(const RowConfig &c, bool vec) {
@@ -284,7 +265,16 @@ SoftFn soft_fn(const RowConfig &c, bool vec) {
   return c.threads <= 512 ? soft_for<512>(c.v, vec, exact) : soft_for<kMaxRowThreads>(c.v, vec, exact);
 }
 
-FusedFn fused_fn(const RowConfig &c, bool vec) { return fused_for(c.v, vec, vec && c.exact); }
+FusedFn fused_fn(const RowConfig &c, bool vec, bool nt) {
+  return nt ? fused_for<true>(c, vec) : fused_for<false>(c, vec);
+}
+
+// Workgroups of the fused launch: one per rmsnorm and softmax row, then one
+// per lanes / 64 matrix rows.
+long long fused_items(const RowConfig &c, int rms_rows, int softmax_rows, int matmul_rows) {
+  const int per_block = c.threads / L2C_WAVE;
+  return static_cast<long long>(rms_rows) + softmax_rows + (static_cast<long long>(matmul_rows) + per_block - 1) / per_block;
+}
 
 }  // namespace
 
@@ -330,9 +320,7 @@ extern "C" int l2c_matvec(float *out, const float *x, const float *W, int cols, 
   } else {
     const bool vec = cols % 4 == 0 && l2c_aligned16(x) && l2c_aligned16(W);
     const dim3 grid((rows + kMatvecWaves - 1) / kMatvecWaves), block(kMatvecWaves * L2C_WAVE);
-    const unsigned long long w_bytes = 4ULL * static_cast<unsigned long long>(rows) * cols;
-    const bool mall = w_bytes > (128ULL << 20) && w_bytes <= (256ULL << 20);
-    if (vec && mall)
+    if (vec && !matvec_nontemporal(cols, rows))
       hipLaunchKernelGGL((matvec_wave_kernel<true, false>), grid, block, 0, stream, out, x, W, cols, rows);
     else if (vec)
       hipLaunchKernelGGL((matvec_wave_kernel<true, true>), grid, block, 0, stream, out, x, W, cols, rows);
@@ -348,21 +336,22 @@ extern "C" int l2c_fused(float *normalized, const float *input, const float *wei
                          float *softmax, const float *logits, float *product,
                          const float *matrix, int size, int rms_rows, int softmax_rows,
                          int matmul_rows, float eps, hipStream_t stream) {
-  if (size <= 0 || rms_rows < 0 || softmax_rows < 0 || matmul_rows < 0)
+  // Matrix row indexes (block x rows per block + wave) stay below INT_MAX.
+  if (size <= 0 || rms_rows < 0 || softmax_rows < 0 || matmul_rows < 0 || matmul_rows > 0x7fffffff - 64)
     return hipErrorInvalidValue;
-  const long long items = static_cast<long long>(rms_rows) + softmax_rows + matmul_rows;
+  const RowConfig cfg = choose_row_config(size);
+  const long long items = fused_items(cfg, rms_rows, softmax_rows, matmul_rows);
   if (items == 0) return hipSuccess;
   if (items > 0x7fffffffLL) return hipErrorInvalidValue;
   if (rms_rows > 0 && (!normalized || !input || !weight)) return hipErrorInvalidValue;
   if (softmax_rows > 0 && (!softmax || !logits)) return hipErrorInvalidValue;
   if (matmul_rows > 0 && (!product || !matrix || !input)) return hipErrorInvalidValue;
-  const RowConfig cfg = choose_row_config(size, kFusedThreads);
   auto ok = [](const void *p) { return p == nullptr || l2c_aligned16(p); };
   const bool vec = size % 4 == 0 && ok(normalized) && ok(input) && ok(weight) && ok(softmax) &&
                    ok(logits) && ok(matrix);
-  hipLaunchKernelGGL(fused_fn(cfg, vec), dim3(static_cast<unsigned>(items)), dim3(cfg.threads),
-                     0, stream, normalized, input, weight, softmax, logits, product, matrix, size,
-                     rms_rows, softmax_rows, eps);
+  hipLaunchKernelGGL(fused_fn(cfg, vec, matvec_nontemporal(size, matmul_rows)),
+                     dim3(static_cast<unsigned>(items)), dim3(cfg.threads), 0, stream, normalized, input,
+                     weight, softmax, logits, product, matrix, size, rms_rows, softmax_rows, matmul_rows, eps);
   L2C_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -405,9 +394,9 @@ extern "C" int l2c_launch_shape(int op, int batch, int cols, int rows, int varia
       }
       break;
     case L2C_OP_FUSED: {
-      const RowConfig cfg = choose_row_config(cols, kFusedThreads);
-      fn = reinterpret_cast<const void *>(fused_fn(cfg, cols % 4 == 0));
-      *grid = 2 * batch + rows;
+      const RowConfig cfg = choose_row_config(cols);
+      fn = reinterpret_cast<const void *>(fused_fn(cfg, cols % 4 == 0, matvec_nontemporal(cols, rows)));
+      *grid = static_cast<int>(fused_items(cfg, batch, batch, rows));
       *block = cfg.threads;
       break;
     }

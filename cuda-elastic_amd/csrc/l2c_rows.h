@@ -1,5 +1,5 @@
 // Device code of the row operations (rmsnorm, softmax, one matrix row dotted
-// with x), shared by the row kernels, the fused kernel and their tuning runs.
+// with x), shared by the row kernels and the fused kernel.
 //
 // A T-lane workgroup holds a row in VGPRs: lane t owns chunk c = t + i*T for
 // i < V, a float4 (VEC) or, for rows that are not 16-byte aligned, four
@@ -187,36 +187,57 @@ __device__ __forceinline__ void softmax_apply_1r(Row<V, VEC, EXACT> &r, float *o
   r.store_scaled(out, size, exp_nonpositive(m - M) / S, nullptr);
 }
 
-// Dot product of one matrix row with x by a whole block: the matrix row is
-// loaded first (all V loads in flight), x is read per chunk.
-template <int V, bool VEC, bool EXACT>
-__device__ __forceinline__ void matvec_row_block(float *out_elem, const float *mrow,
-                                                 const float *x, int size, float *slots) {
-  Row<V, VEC, EXACT> w;
-  w.load(mrow, size, 0.0f);
-  const int T = blockDim.x, t = threadIdx.x;
-  float acc = 0.0f;
-#pragma unroll
-  for (int i = 0; i < V; ++i) {
-    float4 v;
-    if constexpr (VEC) {
-      const int c = t + i * T;
-      if constexpr (EXACT) v = reinterpret_cast<const float4 *>(x)[c];
-      else v = c < (size >> 2) ? reinterpret_cast<const float4 *>(x)[c] : make_float4(0, 0, 0, 0);
-    } else {
-      const int j0 = t + (4 * i) * T;
-      v.x = j0 < size ? x[j0] : 0.0f;
-      v.y = j0 + T < size ? x[j0 + T] : 0.0f;
-      v.z = j0 + 2 * T < size ? x[j0 + 2 * T] : 0.0f;
-      v.w = j0 + 3 * T < size ? x[j0 + 3 * T] : 0.0f;
+// Dot product of matrix row `row` with x by one wavefront: 64 lanes x 16 B =
+// 1 KiB contiguous per load instruction, four independent loads in flight per
+// lane, one wave reduction; lane 0 writes out[row]. NT selects nontemporal
+// loads of the matrix (they keep it from evicting x from L2); ordinary loads
+// let the MALL keep a matrix that fits it between launches. The standalone
+// product and the fused iteration both call this, so their outputs agree bit
+// for bit.
+template <bool VEC, bool NT>
+__device__ __forceinline__ void matvec_wave_row(float *out, const float *x, const float *W, int cols,
+                                                int row, int lane) {
+  const float *w = W + static_cast<size_t>(row) * cols;
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  if constexpr (VEC) {
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    const int cols4 = cols >> 2;
+    int c = lane;
+    for (; c + 3 * L2C_WAVE < cols4; c += 4 * L2C_WAVE) {
+      const float4 m0 = NT ? ld4_stream(w4 + c) : w4[c];
+      const float4 m1 = NT ? ld4_stream(w4 + c + L2C_WAVE) : w4[c + L2C_WAVE];
+      const float4 m2 = NT ? ld4_stream(w4 + c + 2 * L2C_WAVE) : w4[c + 2 * L2C_WAVE];
+      const float4 m3 = NT ? ld4_stream(w4 + c + 3 * L2C_WAVE) : w4[c + 3 * L2C_WAVE];
+      const float4 v0 = x4[c], v1 = x4[c + L2C_WAVE];
+      const float4 v2 = x4[c + 2 * L2C_WAVE], v3 = x4[c + 3 * L2C_WAVE];
+      a0 = fmaf(m0.x, v0.x, a0); a0 = fmaf(m0.y, v0.y, a0);
+      a0 = fmaf(m0.z, v0.z, a0); a0 = fmaf(m0.w, v0.w, a0);
+      a1 = fmaf(m1.x, v1.x, a1); a1 = fmaf(m1.y, v1.y, a1);
+      a1 = fmaf(m1.z, v1.z, a1); a1 = fmaf(m1.w, v1.w, a1);
+      a2 = fmaf(m2.x, v2.x, a2); a2 = fmaf(m2.y, v2.y, a2);
+      a2 = fmaf(m2.z, v2.z, a2); a2 = fmaf(m2.w, v2.w, a2);
+      a3 = fmaf(m3.x, v3.x, a3); a3 = fmaf(m3.y, v3.y, a3);
+      a3 = fmaf(m3.z, v3.z, a3); a3 = fmaf(m3.w, v3.w, a3);
     }
-    acc = fmaf(w.x[i].x, v.x, acc);
-    acc = fmaf(w.x[i].y, v.y, acc);
-    acc = fmaf(w.x[i].z, v.z, acc);
-    acc = fmaf(w.x[i].w, v.w, acc);
+    for (; c < cols4; c += L2C_WAVE) {
+      const float4 m0 = ld4_stream(w4 + c);
+      const float4 v0 = x4[c];
+      a0 = fmaf(m0.x, v0.x, a0); a0 = fmaf(m0.y, v0.y, a0);
+      a0 = fmaf(m0.z, v0.z, a0); a0 = fmaf(m0.w, v0.w, a0);
+    }
+  } else {
+    int c = lane;
+    for (; c + 3 * L2C_WAVE < cols; c += 4 * L2C_WAVE) {
+      a0 = fmaf(__builtin_nontemporal_load(w + c), x[c], a0);
+      a1 = fmaf(__builtin_nontemporal_load(w + c + L2C_WAVE), x[c + L2C_WAVE], a1);
+      a2 = fmaf(__builtin_nontemporal_load(w + c + 2 * L2C_WAVE), x[c + 2 * L2C_WAVE], a2);
+      a3 = fmaf(__builtin_nontemporal_load(w + c + 3 * L2C_WAVE), x[c + 3 * L2C_WAVE], a3);
+    }
+    for (; c < cols; c += L2C_WAVE) a0 = fmaf(__builtin_nontemporal_load(w + c), x[c], a0);
   }
-  acc = block_sum(acc, slots);
-  if (threadIdx.x == 0) *out_elem = acc;
+  const float acc = wave_sum((a0 + a1) + (a2 + a3));
+  if (lane == 0) out[row] = acc;
 }
 
 // Two-pass versions for rows longer than the register-resident limit.
@@ -240,14 +261,6 @@ __device__ inline void softmax_row_generic(float *out, const float *logits, int 
   const float inv = 1.0f / s;
   // Separate loops so the kernel is also correct in place (out == logits).
   for (int j = threadIdx.x; j < size; j += blockDim.x) out[j] = expf(logits[j] - m) * inv;
-}
-
-__device__ inline void matvec_row_block_generic(float *out_elem, const float *mrow,
-                                                const float *x, int size, float *slots) {
-  float acc = 0.0f;
-  for (int j = threadIdx.x; j < size; j += blockDim.x) acc = fmaf(mrow[j], x[j], acc);
-  acc = block_sum(acc, slots);
-  if (threadIdx.x == 0) *out_elem = acc;
 }
 
 }  // namespace l2c

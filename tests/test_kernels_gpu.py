@@ -169,6 +169,33 @@ def test_fused_partial_items(torch_gpu, l2c, orc):
             assert np.all(np.isnan(pp))
 
 
+@pytest.mark.parametrize("batch,size,rows", [
+    (8, 768, 2048), (1, 4096, 11008), (4, 16384, 1024), (1024, 16384, 64), (2, 32768, 64),
+    (2, 65536, 64), (1, 70000, 9), (33, 1001, 77), (3, 1, 5)])
+def test_fused_equals_separate_launches(torch_gpu, l2c, orc, batch, size, rows):
+    """The fused launch runs the row kernels' and the coalesced product's own code
+    in one grid, so its outputs equal the three separate launches' bit for bit:
+    every row-kernel lane count (192 to 1024 lanes, 1 to 16 float4 a lane), the
+    two-pass and unaligned paths, and both matrix load choices (the 172 MiB
+    matrix of 4096 x 11008 is read with ordinary loads)."""
+    torch = torch_gpu
+    print(f"case fused==separate batch={batch} size={size} rows={rows}", flush=True)
+    inp = orc.fill("random", 5, batch, size, rows)
+    x, p, w, M = (dev(torch, a) for a in (inp.input, inp.probabilities, inp.weight, inp.matrix))
+    outs = [(torch.full_like(x, float("nan")), torch.full_like(p, float("nan")),
+             torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")) for _ in range(2)]
+    (n0, s0, g0), (n1, s1, g1) = outs
+    l2c.fused(n0, x, w, s0, p, g0, M, size, batch, batch, rows)
+    l2c.rmsnorm(n1, x, w, size, batch)
+    l2c.softmax(s1, p, size, batch)
+    l2c.matvec(g1, x, M, size, rows, l2c.MATVEC_COALESCED)
+    torch.cuda.synchronize()
+    for a, b in ((n0, n1), (s0, s1), (g0, g1)):
+        np.testing.assert_array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32))
+    ok, err = orc.check_vectors(False, inp, n0.cpu().numpy(), s0.cpu().numpy(), batch, size)
+    assert ok, err
+
+
 @pytest.mark.parametrize("batch,size,rows", [(1, 288, 288), (8, 768, 2048), (64, 1000, 300),
                                              (33, 1001, 77), (256, 512, 128), (300, 96, 200),
                                              (512, 2048, 1024), (2, 5, 3), (3, 20, 5),
