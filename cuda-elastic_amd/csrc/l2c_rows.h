@@ -121,36 +121,6 @@ __device__ __forceinline__ float exp_nonpositive(float t) {
   return t < -104.0f ? 0.0f : e;
 }
 
-template <int V, bool VEC, bool EXACT, bool FAST_EXP = false>
-__device__ __forceinline__ void softmax_apply(Row<V, VEC, EXACT> &r, float *out, int size,
-                                              float *slots) {
-  float m = -FLT_MAX;
-#pragma unroll
-  for (int i = 0; i < V; ++i)
-    m = fmaxf(m, fmaxf(fmaxf(r.x[i].x, r.x[i].y), fmaxf(r.x[i].z, r.x[i].w)));
-  m = block_max(m, slots);
-  // exp of padding (-FLT_MAX - m) underflows to exactly 0.
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < V; ++i) {
-    if constexpr (FAST_EXP) {
-      r.x[i].x = exp_nonpositive(r.x[i].x - m);
-      r.x[i].y = exp_nonpositive(r.x[i].y - m);
-      r.x[i].z = exp_nonpositive(r.x[i].z - m);
-      r.x[i].w = exp_nonpositive(r.x[i].w - m);
-    } else {
-      r.x[i].x = expf(r.x[i].x - m);
-      r.x[i].y = expf(r.x[i].y - m);
-      r.x[i].z = expf(r.x[i].z - m);
-      r.x[i].w = expf(r.x[i].w - m);
-    }
-    s += (r.x[i].x + r.x[i].y) + (r.x[i].z + r.x[i].w);
-  }
-  s = block_sum(s, slots + 16);
-  const float inv = 1.0f / s;
-  r.store_scaled(out, size, inv, nullptr);
-}
-
 // softmax with a single block reduction: each wavefront exponentiates
 // against its own maximum m_w and sums (s_w); the waves' (m_w, s_w) pairs
 // meet once in LDS, every lane combines them in wave order into the row

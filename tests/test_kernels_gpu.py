@@ -98,7 +98,7 @@ def test_large_logits_range(torch_gpu, l2c, orc):
     assert np.all(np.isfinite(got)) and np.all(got >= 0)
 
 
-MATVEC_SHAPES = [(288, 288), (4096, 11008), (768, 2048), (1000, 300), (1001, 77), (16384, 257),
+MATVEC_SHAPES = [(288, 288), (4096, 11008), (768, 2048), (1000, 300), (1001, 77), (16384, 257), (16388, 20), (32768, 33),
                  (1, 5), (7, 1)]
 
 
@@ -170,8 +170,9 @@ def test_fused_partial_items(torch_gpu, l2c, orc):
 
 
 @pytest.mark.parametrize("batch,size,rows", [
-    (8, 768, 2048), (1, 4096, 11008), (4, 16384, 1024), (1024, 16384, 64), (2, 32768, 64),
-    (2, 65536, 64), (1, 70000, 9), (33, 1001, 77), (3, 1, 5)])
+    (8, 768, 2048), (1, 4096, 11008), (4, 16384, 1024), (1024, 16384, 64), (5, 16384, 7),
+    (3, 16388, 50), (2, 32768, 64), (2, 65536, 64), (1, 70000, 9), (2, 16385, 10), (33, 1001, 77),
+    (3, 1, 5)])
 def test_fused_equals_separate_launches(torch_gpu, l2c, orc, batch, size, rows):
     """The fused launch runs the row kernels' and the coalesced product's own code
     in one grid, so its outputs equal the three separate launches' bit for bit:
@@ -194,6 +195,33 @@ def test_fused_equals_separate_launches(torch_gpu, l2c, orc, batch, size, rows):
         np.testing.assert_array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32))
     ok, err = orc.check_vectors(False, inp, n0.cpu().numpy(), s0.cpu().numpy(), batch, size)
     assert ok, err
+
+
+@pytest.mark.parametrize("size", [16384, 16388, 70000])
+def test_fused_partial_items_long_rows(torch_gpu, l2c, orc, size):
+    """Fused launches with differing row counts on rows of 512 and 576 lanes and
+    on the two-pass path: the rows computed equal the separate launches' bit for
+    bit and nothing else is written."""
+    torch = torch_gpu
+    inp = orc.fill("random", 6, 7, size, 9)
+    x, p, w, M = (dev(torch, a) for a in (inp.input, inp.probabilities, inp.weight, inp.matrix))
+    n1, s1 = torch.empty_like(x), torch.empty_like(p)
+    g1 = torch.empty((9,), dtype=torch.float32, device="cuda")
+    l2c.rmsnorm(n1, x, w, size, 7)
+    l2c.softmax(s1, p, size, 7)
+    l2c.matvec(g1, x, M, size, 9, l2c.MATVEC_COALESCED)
+    ref = [t.cpu().numpy().view(np.uint32) for t in (n1, s1, g1)]
+    for rr, sr, mr in [(5, 2, 9), (1, 6, 0), (0, 0, 9), (7, 0, 0), (3, 3, 1)]:
+        print(f"case fused partial size={size} rms={rr} softmax={sr} matmul={mr}", flush=True)
+        n = torch.full_like(x, float("nan"))
+        s = torch.full_like(p, float("nan"))
+        prod = torch.full((9,), float("nan"), dtype=torch.float32, device="cuda")
+        l2c.fused(n, x, w, s, p, prod, M, size, rr, sr, mr)
+        torch.cuda.synchronize()
+        for got, want, k in ((n, ref[0], rr * size), (s, ref[1], sr * size), (prod, ref[2], mr)):
+            g = got.cpu().numpy()
+            np.testing.assert_array_equal(g[:k].view(np.uint32), want[:k])
+            assert np.all(np.isnan(g[k:]))
 
 
 @pytest.mark.parametrize("batch,size,rows", [(1, 288, 288), (8, 768, 2048), (64, 1000, 300),
