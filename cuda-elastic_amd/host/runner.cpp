@@ -96,7 +96,7 @@ struct PinnedBuffer {
 
 struct Streams {
   hipStream_t rms = nullptr, soft = nullptr, mm = nullptr;
-  hipEvent_t fork = nullptr, soft_done = nullptr, mm_done = nullptr;
+  hipEvent_t fork = nullptr, rms_done = nullptr, soft_done = nullptr;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   hipEvent_t marks[kOpWindows + 1] = {};
   hipGraph_t graph = nullptr;
@@ -104,7 +104,7 @@ struct Streams {
   ~Streams() {
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
-    for (hipEvent_t e : {fork, soft_done, mm_done, t0, t1})
+    for (hipEvent_t e : {fork, rms_done, soft_done, t0, t1})
       if (e) (void)hipEventDestroy(e);
     for (hipEvent_t e : marks)
       if (e) (void)hipEventDestroy(e);
@@ -202,8 +202,8 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
     HIP_OK(hipStreamCreateWithFlags(&st.soft, hipStreamNonBlocking));
     HIP_OK(hipStreamCreateWithFlags(&st.mm, hipStreamNonBlocking));
     HIP_OK(hipEventCreateWithFlags(&st.fork, hipEventDisableTiming));
+    HIP_OK(hipEventCreateWithFlags(&st.rms_done, hipEventDisableTiming));
     HIP_OK(hipEventCreateWithFlags(&st.soft_done, hipEventDisableTiming));
-    HIP_OK(hipEventCreateWithFlags(&st.mm_done, hipEventDisableTiming));
     HIP_OK(hipEventCreate(&st.t0));
     HIP_OK(hipEventCreate(&st.t1));
 
@@ -292,7 +292,7 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
         kernels_per_rep * o.repeats +
         (o.copy_outputs ? (o.host_write ? 3 : 0) + (mm == Matmul::kFused && !o.one_stream ? 1 : 0) : 0);
 
-    // One iteration. Three-stream variants: fork from the rmsnorm stream,
+    // One iteration. Three-stream variants: fork from the product's stream,
     // `repeats` x {rmsnorm | softmax | matmul} on their streams, copies on
     // the last repeat in copy mode, join back (llama2c_cuda_graph.cu:347-381).
     // Fused: one launch per repeat; in copy mode the last repeat runs the
@@ -338,9 +338,15 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
         }
         return;
       }
-      HIP_OK(hipEventRecord(st.fork, st.rms));
+      // Fork from and join back to the product's stream: the path from one
+      // product to the next (product, join, fork, product) then stays on one
+      // stream, and only the short rmsnorm and softmax rows wait on the other
+      // streams' events. Same dependencies as forking from the rmsnorm stream
+      // (llama2c_cuda_graph.cu:347-381); at C4 it saves the direct iteration
+      // the two cross-stream hops the product would otherwise wait for.
+      HIP_OK(hipEventRecord(st.fork, st.mm));
+      HIP_OK(hipStreamWaitEvent(st.rms, st.fork, 0));
       HIP_OK(hipStreamWaitEvent(st.soft, st.fork, 0));
-      HIP_OK(hipStreamWaitEvent(st.mm, st.fork, 0));
       for (int rep = 0; rep < o.repeats; ++rep) {
         // The product first: its workgroups take their CUs at once, and the
         // rmsnorm and softmax rows fill the slots its workgroups leave free
@@ -354,26 +360,29 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
           d2h(h_product.ptr, d_product.ptr, prod_elems, st.mm);
         }
       }
+      HIP_OK(hipEventRecord(st.rms_done, st.rms));
       HIP_OK(hipEventRecord(st.soft_done, st.soft));
-      HIP_OK(hipEventRecord(st.mm_done, st.mm));
-      HIP_OK(hipStreamWaitEvent(st.rms, st.soft_done, 0));
-      HIP_OK(hipStreamWaitEvent(st.rms, st.mm_done, 0));
+      HIP_OK(hipStreamWaitEvent(st.mm, st.rms_done, 0));
+      HIP_OK(hipStreamWaitEvent(st.mm, st.soft_done, 0));
     };
+    // The stream an iteration starts and ends on: the product's for the
+    // three-stream form, the rmsnorm stream for the one-stream and fused forms.
+    const hipStream_t home = o.one_stream || mm == Matmul::kFused ? st.rms : st.mm;
 
     if (o.graph) {
       auto t = std::chrono::steady_clock::now();
       range_push("llama2c.graph_capture");
-      HIP_OK(hipStreamBeginCapture(st.rms, hipStreamCaptureModeGlobal));
+      HIP_OK(hipStreamBeginCapture(home, hipStreamCaptureModeGlobal));
       enqueue_iteration();
-      HIP_OK(hipStreamEndCapture(st.rms, &st.graph));
+      HIP_OK(hipStreamEndCapture(home, &st.graph));
       range_pop();
       res->graph_capture_ms = ms_since(t);
       t = std::chrono::steady_clock::now();
       HIP_OK(hipGraphInstantiate(&st.exec, st.graph, nullptr, nullptr, 0));
       res->graph_instantiate_ms = ms_since(t);
       t = std::chrono::steady_clock::now();
-      HIP_OK(hipGraphUpload(st.exec, st.rms));
-      HIP_OK(hipStreamSynchronize(st.rms));
+      HIP_OK(hipGraphUpload(st.exec, home));
+      HIP_OK(hipStreamSynchronize(home));
       res->graph_upload_ms = ms_since(t);
     } else {
       kernels_per_iter = kernels_per_iter_planned;
@@ -381,7 +390,7 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
     res->kernels_per_iter = kernels_per_iter;
 
     auto run_iteration = [&]() {
-      if (o.graph) HIP_OK(hipGraphLaunch(st.exec, st.rms));
+      if (o.graph) HIP_OK(hipGraphLaunch(st.exec, home));
       else enqueue_iteration();
     };
     auto synchronize_all = [&]() {
@@ -413,7 +422,7 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
     res->launches = launches;
 
     // Back-to-back loop (llama2c_cuda_graph.cu:433-456).
-    HIP_OK(hipEventRecord(st.t0, st.rms));
+    HIP_OK(hipEventRecord(st.t0, home));
     const auto wall_start = std::chrono::steady_clock::now();
     for (int i = 0; i < launches; ++i) {
       range_push("llama2c.iteration");
@@ -421,7 +430,7 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
       range_pop();
     }
     res->submit_us = 1000.0 * ms_since(wall_start);
-    HIP_OK(hipEventRecord(st.t1, st.rms));
+    HIP_OK(hipEventRecord(st.t1, home));
     synchronize_all();
     res->wall_ms = ms_since(wall_start);
     float gpu_ms = 0.0f;
@@ -433,9 +442,9 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
     for (int i = 0; i < kSingleIterations; ++i) {
       synchronize_all();
       range_push("llama2c.single");
-      HIP_OK(hipEventRecord(st.t0, st.rms));
+      HIP_OK(hipEventRecord(st.t0, home));
       run_iteration();
-      HIP_OK(hipEventRecord(st.t1, st.rms));
+      HIP_OK(hipEventRecord(st.t1, home));
       range_pop();
       HIP_OK(hipEventSynchronize(st.t1));
       float ms = 0.0f;
