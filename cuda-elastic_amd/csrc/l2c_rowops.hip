@@ -236,21 +236,26 @@ FusedFn fused_pick(bool vec, bool exact) {
   return exact ? fused_kernel<V, true, true, MAXT, NT> : fused_kernel<V, true, false, MAXT, NT>;
 }
 
+// Any other pair gets no instance (null).
 template <bool NT>
 FusedFn fused_for(const RowConfig &c, bool vec) {
   const bool exact = vec && c.exact;
   if (c.v == 0)
-    return vec ? fused_kernel<0, true, false, kGenericThreads, NT> : fused_kernel<0, false, false, kGenericThreads, NT>;
+    return c.threads == kGenericThreads ? (vec ? fused_kernel<0, true, false, kGenericThreads, NT>
+                                               : fused_kernel<0, false, false, kGenericThreads, NT>)
+                                        : nullptr;
   if (c.threads <= 256) {
     switch (c.v) {
       case 1: return fused_pick<1, 256, NT>(vec, exact);
       case 2: return fused_pick<2, 256, NT>(vec, exact);
       case 4: return fused_pick<4, 256, NT>(vec, exact);
-      default: return fused_pick<8, 256, NT>(vec, exact);
+      case 8: return fused_pick<8, 256, NT>(vec, exact);
+      default: return nullptr;
     }
   }
-  if (c.threads <= 512) return fused_pick<8, 512, NT>(vec, exact);
-  return c.v == 8 ? fused_pick<8, kMaxRowThreads, NT>(vec, exact) : fused_pick<16, kMaxRowThreads, NT>(vec, exact);
+  if (c.threads <= 512) return c.v == 8 ? fused_pick<8, 512, NT>(vec, exact) : nullptr;
+  if (c.v == 8) return fused_pick<8, kMaxRowThreads, NT>(vec, exact);
+  return c.v == 16 ? fused_pick<16, kMaxRowThreads, NT>(vec, exact) : nullptr;
 }
 
 RmsFn rms_fn(const RowConfig &c, bool vec) {
@@ -349,7 +354,9 @@ extern "C" int l2c_fused(float *normalized, const float *input, const float *wei
   auto ok = [](const void *p) { return p == nullptr || l2c_aligned16(p); };
   const bool vec = size % 4 == 0 && ok(normalized) && ok(input) && ok(weight) && ok(softmax) &&
                    ok(logits) && ok(matrix);
-  hipLaunchKernelGGL(fused_fn(cfg, vec, matvec_nontemporal(size, matmul_rows)),
+  const FusedFn fn = fused_fn(cfg, vec, matvec_nontemporal(size, matmul_rows));
+  if (!fn) return hipErrorNotSupported;
+  hipLaunchKernelGGL(fn,
                      dim3(static_cast<unsigned>(items)), dim3(cfg.threads), 0, stream, normalized, input,
                      weight, softmax, logits, product, matrix, size, rms_rows, softmax_rows, matmul_rows, eps);
   L2C_LAUNCH_CHECK();
@@ -396,7 +403,9 @@ extern "C" int l2c_launch_shape(int op, int batch, int cols, int rows, int varia
     case L2C_OP_FUSED: {
       const RowConfig cfg = choose_row_config(cols);
       fn = reinterpret_cast<const void *>(fused_fn(cfg, cols % 4 == 0, matvec_nontemporal(cols, rows)));
-      *grid = static_cast<int>(fused_items(cfg, batch, batch, rows));
+      const long long items = fused_items(cfg, batch, batch, rows);
+      if (!fn || items > 0x7fffffffLL) return hipErrorInvalidValue;
+      *grid = static_cast<int>(items);
       *block = cfg.threads;
       break;
     }

@@ -197,6 +197,20 @@ def test_fused_equals_separate_launches(torch_gpu, l2c, orc, batch, size, rows):
     assert ok, err
 
 
+def test_fused_launch_shape_every_row_size(torch_gpu, l2c):
+    """Every row size maps to a fused kernel instance of the row kernels' size,
+    and the launch takes one workgroup per rmsnorm and softmax row plus one per
+    lanes / 64 matrix rows."""
+    sizes = list(range(1, 300)) + [767, 768, 1000, 1001, 4095, 4096, 4097, 8192, 8196, 16380, 16384,
+                                   16388, 20000, 32768, 32772, 65536, 65537, 70000, 100000]
+    for size in sizes:
+        grid, block, per_cu = l2c.launch_shape(l2c.OP_FUSED, 3, size, 1000)
+        rgrid, rblock, _ = l2c.launch_shape(l2c.OP_RMSNORM, 3, size, 1)
+        assert block == rblock, (size, block, rblock)
+        assert grid == 6 + -(-1000 // (block // 64)), (size, grid, block)
+        assert per_cu >= 1, size
+
+
 @pytest.mark.parametrize("size", [16384, 16388, 70000])
 def test_fused_partial_items_long_rows(torch_gpu, l2c, orc, size):
     """Fused launches with differing row counts on rows of 512 and 576 lanes and
