@@ -42,6 +42,13 @@
 // random operands with one wave per SIMD (256-lane blocks). The
 // random-operand rate is the one real data meets (the matrix cores' power
 // draw depends on the operand bits).
+//
+//   l2c_kernel_bench lds
+// measures the LDS read rate per CU that the contractions' fragment reads
+// draw on: one 96 KB block per CU (so no two share a CU) reads a 64 KB LDS
+// array with ds_read_b128 or ds_read_b64, eight loads in flight per wave
+// between waits, at 4, 8 and 16 waves per CU; bytes per shader clock per CU
+// from the shader cycle counter, the clock from the fixed-rate wall clock.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -355,10 +362,90 @@ static int run_ceilings() {
   return 0;
 }
 
+// LDS read rate. Every lane reads BYTES at offsets that are multiples of
+// BYTES inside the 64 KB it initialises, so each access is in bounds; the
+// reads are volatile so the loop cannot be folded.
+template <int BYTES>
+__global__ __launch_bounds__(1024) void lds_read_kernel(unsigned *out, unsigned long long *clk, int iters) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[96 * 1024];  // 64 KB used
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  const int t = threadIdx.x;
+  for (int i = t * 4; i < 65536; i += blockDim.x * 4) *reinterpret_cast<unsigned *>(lds + i) = i * 2654435761u;
+  __syncthreads();
+  const unsigned long long c0 = clock64(), w0 = wall_clock64();
+  unsigned acc = 0, off = (t * BYTES) & 65535u;
+  for (int it = 0; it < iters; ++it) {
+    if constexpr (BYTES == 16) {
+      u32x4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        asm volatile("ds_read_b128 %0, %1" : "=v"(v[u]) : "v"((off + u * 4096u) & 65535u) : "memory");
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc ^= v[u][0] ^ v[u][3];
+    } else {
+      u32x2 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        asm volatile("ds_read_b64 %0, %1" : "=v"(v[u]) : "v"((off + u * 4096u) & 65535u) : "memory");
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc ^= v[u][0] ^ v[u][1];
+    }
+    off = (off + 32768u) & 65535u;
+  }
+  const unsigned long long c1 = clock64(), w1 = wall_clock64();
+  out[blockIdx.x * blockDim.x + t] = acc;
+  if (t == 0) {
+    clk[2 * blockIdx.x] = c1 - c0;
+    clk[2 * blockIdx.x + 1] = w1 - w0;
+  }
+}
+
+static int run_lds() {
+  int cus = 0, wall_khz = 0;
+  CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+  CHECK(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, 0));
+  const int iters = 4096;
+  unsigned *out = nullptr;
+  unsigned long long *clk = nullptr;
+  CHECK(hipMalloc(&out, static_cast<size_t>(cus) * 1024 * 4));
+  CHECK(hipMalloc(&clk, static_cast<size_t>(cus) * 2 * 8));
+  std::vector<unsigned long long> h(2 * static_cast<size_t>(cus));
+  for (int threads : {256, 512, 1024}) {
+    for (int bytes : {16, 8}) {
+      for (int pass = 0; pass < 2; ++pass) {  // the second pass is reported
+        if (bytes == 16)
+          hipLaunchKernelGGL(lds_read_kernel<16>, dim3(cus), dim3(threads), 0, nullptr, out, clk, iters);
+        else
+          hipLaunchKernelGGL(lds_read_kernel<8>, dim3(cus), dim3(threads), 0, nullptr, out, clk, iters);
+        CHECK(hipGetLastError());
+        CHECK(hipDeviceSynchronize());
+      }
+      CHECK(hipMemcpy(h.data(), clk, h.size() * 8, hipMemcpyDeviceToHost));
+      std::vector<double> cycles, ghz;
+      for (int b = 0; b < cus; ++b) {
+        cycles.push_back(static_cast<double>(h[2 * b]));
+        ghz.push_back(static_cast<double>(h[2 * b]) / (static_cast<double>(h[2 * b + 1]) / (wall_khz * 1e3)) / 1e9);
+      }
+      std::sort(cycles.begin(), cycles.end());
+      std::sort(ghz.begin(), ghz.end());
+      const double bytes_per_block = static_cast<double>(iters) * 8 * threads * bytes;
+      std::printf("lds read=b%d waves_per_cu=%d bytes_per_clk_per_cu=%.1f clock_ghz=%.2f\n", bytes * 8, threads / 64,
+                  bytes_per_block / cycles[cus / 2], ghz[cus / 2]);
+    }
+  }
+  CHECK(hipFree(out));
+  CHECK(hipFree(clk));
+  return 0;
+}
+
 int main(int argc, char **argv) {
   if (argc == 2 && std::strcmp(argv[1], "ceiling") == 0) return run_ceilings();
+  if (argc == 2 && std::strcmp(argv[1], "lds") == 0) return run_lds();
   if (argc != 6) {
-    std::fprintf(stderr, "Usage: %s OP BATCH SIZE ROWS ITERS | %s ceiling\n", argv[0], argv[0]);
+    std::fprintf(stderr, "Usage: %s OP BATCH SIZE ROWS ITERS | %s ceiling | %s lds\n", argv[0], argv[0], argv[0]);
     return 2;
   }
   const std::string op = argv[1];

@@ -63,3 +63,19 @@ def test_mfma_ceilings(torch_gpu):
         assert 0.0 < rates["random_tflops"] <= rates["constant_tflops"] * 1.02, ln
         assert 0.5 * peak < rates["constant_tflops"] <= 1.02 * peak, ln
         assert 0.0 < rates["random_one_wave_tflops"] <= 1.02 * peak, ln
+
+
+def test_lds_read_rates(torch_gpu):
+    # Six lines (b128 / b64 at 4, 8, 16 waves a CU); a rate in bytes per shader
+    # clock per CU that grows with the waves in flight and stays under 512 B/clk,
+    # and a shader clock within the part's range.
+    r = run("lds", timeout=120)
+    assert r.returncode == 0, r.stderr
+    rates = {}
+    for read, waves, rate, ghz in re.findall(
+            r"lds read=(b128|b64) waves_per_cu=(\d+) bytes_per_clk_per_cu=([0-9.]+) clock_ghz=([0-9.]+)", r.stdout):
+        rates[(read, int(waves))] = float(rate)
+        assert 0.5 < float(ghz) < 2.6, r.stdout
+    assert len(rates) == 6, r.stdout
+    for read in ("b128", "b64"):
+        assert 0.0 < rates[(read, 4)] < rates[(read, 16)] < 512.0, rates
