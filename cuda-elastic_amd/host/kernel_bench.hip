@@ -373,6 +373,8 @@ __global__ __launch_bounds__(1024) void lds_read_kernel(unsigned *out, unsigned 
   const int t = threadIdx.x;
   for (int i = t * 4; i < 65536; i += blockDim.x * 4) *reinterpret_cast<unsigned *>(lds + i) = i * 2654435761u;
   __syncthreads();
+  // ds_read takes an LDS byte address: the array's own address plus the offset.
+  const unsigned base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
   const unsigned long long c0 = clock64(), w0 = wall_clock64();
   unsigned acc = 0, off = (t * BYTES) & 65535u;
   for (int it = 0; it < iters; ++it) {
@@ -380,7 +382,7 @@ __global__ __launch_bounds__(1024) void lds_read_kernel(unsigned *out, unsigned 
       u32x4 v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        asm volatile("ds_read_b128 %0, %1" : "=v"(v[u]) : "v"((off + u * 4096u) & 65535u) : "memory");
+        asm volatile("ds_read_b128 %0, %1" : "=v"(v[u]) : "v"(base + ((off + u * 4096u) & 65535u)) : "memory");
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
       for (int u = 0; u < 8; ++u) acc ^= v[u][0] ^ v[u][3];
@@ -388,7 +390,7 @@ __global__ __launch_bounds__(1024) void lds_read_kernel(unsigned *out, unsigned 
       u32x2 v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        asm volatile("ds_read_b64 %0, %1" : "=v"(v[u]) : "v"((off + u * 4096u) & 65535u) : "memory");
+        asm volatile("ds_read_b64 %0, %1" : "=v"(v[u]) : "v"(base + ((off + u * 4096u) & 65535u)) : "memory");
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
       for (int u = 0; u < 8; ++u) acc ^= v[u][0] ^ v[u][1];
