@@ -147,8 +147,9 @@ def cpu_baseline(batch, size, rows, sample_vectors, repeats=3):
     (OpenMP over rows and vectors): rmsnorm and softmax of every vector and
     the product of sample_vectors of them against all rows, each the median
     of `repeats` runs, the product scaled linearly to the whole batch (every
-    vector costs the same). The double oracle (the validation reference) is
-    timed apart on one thread."""
+    vector costs the same; the bench passes the whole batch, about 10-15 s of
+    host time over the three runs). The double oracle (the validation
+    reference) is timed apart on one thread."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle
@@ -185,7 +186,8 @@ def cpu_baseline(batch, size, rows, sample_vectors, repeats=3):
         "sample": (f"oracle orc_iteration_f32_mt (fp32, llama2.c loop order, {threads} OpenMP threads): "
                    f"rmsnorm+softmax of all {batch} vectors ({t_vec:.3f} s) and the product of "
                    f"{sample_vectors} of {batch} vectors x {rows} rows x {size} ({t_mm:.2f} s), medians "
-                   f"of {repeats}, the product scaled linearly to one {batch}x{size}x{rows} iteration"),
+                   f"of {repeats}" + ("" if sample_vectors == batch else
+                                      f", the product scaled linearly to one {batch}x{size}x{rows} iteration")),
         "double_oracle": {
             "value": t_dbl * batch / dv * 1e6, "unit": "us/iter", "cores": 1,
             "sample": f"orc_product_check (double reference + tolerance) of {dv} vectors x {rows} rows x "
@@ -340,7 +342,7 @@ def main():
     }
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(B, S, R, sample_vectors=256)
+        cpu = cpu_baseline(B, S, R, sample_vectors=B)
         log(f"[bench] cpu baseline {cpu['value'] / 1e6:.1f} s/iter ({cpu['measured_s']:.1f} s measured)")
         cpu.pop("measured_s")
     us = headline["gpu_ms_per_iter"] * 1000.0
