@@ -18,7 +18,8 @@
 //    one-pass structure with scalar loads; rows longer than 1024 lanes x 64
 //    floats take a two-pass path that re-reads the row.
 //  * The coalesced matrix-vector product gives each output row to one
-//    wavefront: 64 lanes x 16 B = 1 KiB contiguous per load instruction,
+//    wavefront (a pair of wavefronts, each half the row, for aligned rows of
+//    >= 8192 floats): 64 lanes x 16 B = 1 KiB contiguous per load instruction,
 //    several independent loads in flight per lane, one wave reduction per row.
 //    W is read with nontemporal loads (they keep it from evicting x from L2),
 //    except when it is 128-256 MiB: then ordinary loads let the 256 MB MALL
@@ -31,8 +32,9 @@
 //    result is bit-reproducible by a CPU fmaf chain.
 //  * The fused iteration is one grid of the standalone kernels' workgroups:
 //    rmsnorm and softmax rows in the row kernels' configuration, then matrix
-//    rows one per wavefront with the standalone product's load choice, so its
-//    outputs equal the three separate launches' bit for bit. At 1024 x 16384
+//    rows one per wavefront (or pair of wavefronts) with the standalone
+//    product's load choice, so its outputs equal the three separate launches'
+//    bit for bit. At 1024 x 16384
 //    x 8192 (one box, alternating runs) it took 123.3 against 135.3 us for
 //    the earlier form that ran every part at 256 lanes (a whole workgroup per
 //    matrix row, rows at 16 float4 a lane).
@@ -45,6 +47,10 @@ using l2c::Row;
 
 constexpr int kMaxRowThreads = 1024;
 constexpr int kGenericThreads = 256;
+// Aligned matrices with at least this many columns are multiplied a row per
+// pair of wavefronts (l2c::matvec_pair_row); narrower ones a row per
+// wavefront (l2c::matvec_wave_row).
+constexpr int kPairCols = 8192;
 
 // ---------------------------------------------------------------------------
 // Kernels. V == 0 selects the two-pass generic path; MAXT is the launch
@@ -88,7 +94,7 @@ template <int V, bool VEC, bool EXACT, int MAXT, bool NT>
 __global__ __launch_bounds__(MAXT) void fused_kernel(
     float *normalized, const float *input, const float *weight, float *softmax,
     const float *logits, float *product, const float *matrix, int size, int rms_rows,
-    int softmax_rows, int matmul_rows, float eps) {
+    int softmax_rows, int matmul_rows, int pair, float eps) {
   __shared__ float slots[32];
   int item = blockIdx.x;
   const int pairs = min(rms_rows, softmax_rows);
@@ -104,11 +110,22 @@ __global__ __launch_bounds__(MAXT) void fused_kernel(
     row = pairs + item;
   } else {
     kind = 2;
-    row = (item - (softmax_rows - pairs)) * (blockDim.x / L2C_WAVE) + threadIdx.x / L2C_WAVE;
+    row = item - (softmax_rows - pairs);  // the matrix workgroup's index
   }
   if (kind == 2) {
-    if (row < matmul_rows)
-      l2c::matvec_wave_row<VEC, NT>(product, input, matrix, size, row, threadIdx.x % L2C_WAVE);
+    const int waves = blockDim.x / L2C_WAVE, wave = threadIdx.x / L2C_WAVE, lane = threadIdx.x % L2C_WAVE;
+    if constexpr (VEC) {
+      if (pair) {
+        // waves / 2 rows a workgroup; a wave left over (odd wave counts) only
+        // takes part in the barrier.
+        const int r = row * (waves / 2) + wave / 2;
+        const bool live = wave < waves / 2 * 2 && r < matmul_rows;
+        l2c::matvec_pair_row<NT>(product, input, matrix, size, r, wave % 2, lane, live, slots);
+        return;
+      }
+    }
+    const int r = row * waves + wave;
+    if (r < matmul_rows) l2c::matvec_wave_row<VEC, NT>(product, input, matrix, size, r, lane);
     return;
   }
   const size_t off = static_cast<size_t>(row) * size;
@@ -149,6 +166,20 @@ __global__ __launch_bounds__(kMatvecWaves * L2C_WAVE) void matvec_wave_kernel(
   if (row < rows) l2c::matvec_wave_row<VEC, NT>(out, x, W, cols, row, threadIdx.x % L2C_WAVE);
 }
 
+// A row per pair of wavefronts, kMatvecWaves / 2 rows a workgroup.
+template <bool NT>
+__global__ __launch_bounds__(kMatvecWaves * L2C_WAVE) void matvec_pair_kernel(
+    float *out, const float *x, const float *W, int cols, int rows) {
+  __shared__ float slots[kMatvecWaves];
+  const int wave = threadIdx.x / L2C_WAVE;
+  const int row = blockIdx.x * (kMatvecWaves / 2) + wave / 2;
+  l2c::matvec_pair_row<NT>(out, x, W, cols, row, wave % 2, threadIdx.x % L2C_WAVE, row < rows, slots);
+}
+
+// The coalesced product's form: a pair of wavefronts per row for aligned rows
+// of >= kPairCols floats, else one wavefront per row.
+bool pair_rows(int cols, bool vec) { return vec && cols >= kPairCols; }
+
 // Nontemporal matrix loads, except for a matrix of 128-256 MiB, which the
 // 256 MB MALL keeps between launches when it is read with ordinary loads.
 bool matvec_nontemporal(int cols, int rows) {
@@ -188,7 +219,7 @@ RowConfig choose_row_config(int size, int max_threads = kMaxRowThreads) {
 using RmsFn = void (*)(float *, const float *, const float *, int, float);
 using SoftFn = void (*)(float *, const float *, int);
 using FusedFn = void (*)(float *, const float *, const float *, float *, const float *, float *,
-                         const float *, int, int, int, int, float);
+                         const float *, int, int, int, int, int, float);
 
 // Kernel instance for (V, vector path, exact, launch bound).
 template <int V, int MAXT>
@@ -275,9 +306,9 @@ FusedFn fused_fn(const RowConfig &c, bool vec, bool nt) {
 }
 
 // Workgroups of the fused launch: one per rmsnorm and softmax row, then one
-// per lanes / 64 matrix rows.
-long long fused_items(const RowConfig &c, int rms_rows, int softmax_rows, int matmul_rows) {
-  const int per_block = c.threads / L2C_WAVE;
+// per lanes / 64 matrix rows (lanes / 128 when a pair of wavefronts takes a row).
+long long fused_items(const RowConfig &c, bool pair, int rms_rows, int softmax_rows, int matmul_rows) {
+  const int per_block = c.threads / L2C_WAVE / (pair ? 2 : 1);
   return static_cast<long long>(rms_rows) + softmax_rows + (static_cast<long long>(matmul_rows) + per_block - 1) / per_block;
 }
 
@@ -325,7 +356,12 @@ extern "C" int l2c_matvec(float *out, const float *x, const float *W, int cols, 
   } else {
     const bool vec = cols % 4 == 0 && l2c_aligned16(x) && l2c_aligned16(W);
     const dim3 grid((rows + kMatvecWaves - 1) / kMatvecWaves), block(kMatvecWaves * L2C_WAVE);
-    if (vec && !matvec_nontemporal(cols, rows))
+    const dim3 pair_grid((rows + kMatvecWaves / 2 - 1) / (kMatvecWaves / 2));
+    if (pair_rows(cols, vec) && !matvec_nontemporal(cols, rows))
+      hipLaunchKernelGGL(matvec_pair_kernel<false>, pair_grid, block, 0, stream, out, x, W, cols, rows);
+    else if (pair_rows(cols, vec))
+      hipLaunchKernelGGL(matvec_pair_kernel<true>, pair_grid, block, 0, stream, out, x, W, cols, rows);
+    else if (vec && !matvec_nontemporal(cols, rows))
       hipLaunchKernelGGL((matvec_wave_kernel<true, false>), grid, block, 0, stream, out, x, W, cols, rows);
     else if (vec)
       hipLaunchKernelGGL((matvec_wave_kernel<true, true>), grid, block, 0, stream, out, x, W, cols, rows);
@@ -345,20 +381,21 @@ extern "C" int l2c_fused(float *normalized, const float *input, const float *wei
   if (size <= 0 || rms_rows < 0 || softmax_rows < 0 || matmul_rows < 0 || matmul_rows > 0x7fffffff - 64)
     return hipErrorInvalidValue;
   const RowConfig cfg = choose_row_config(size);
-  const long long items = fused_items(cfg, rms_rows, softmax_rows, matmul_rows);
+  auto ok = [](const void *p) { return p == nullptr || l2c_aligned16(p); };
+  const bool vec = size % 4 == 0 && ok(normalized) && ok(input) && ok(weight) && ok(softmax) &&
+                   ok(logits) && ok(matrix);
+  const bool pair = pair_rows(size, vec);
+  const long long items = fused_items(cfg, pair, rms_rows, softmax_rows, matmul_rows);
   if (items == 0) return hipSuccess;
   if (items > 0x7fffffffLL) return hipErrorInvalidValue;
   if (rms_rows > 0 && (!normalized || !input || !weight)) return hipErrorInvalidValue;
   if (softmax_rows > 0 && (!softmax || !logits)) return hipErrorInvalidValue;
   if (matmul_rows > 0 && (!product || !matrix || !input)) return hipErrorInvalidValue;
-  auto ok = [](const void *p) { return p == nullptr || l2c_aligned16(p); };
-  const bool vec = size % 4 == 0 && ok(normalized) && ok(input) && ok(weight) && ok(softmax) &&
-                   ok(logits) && ok(matrix);
   const FusedFn fn = fused_fn(cfg, vec, matvec_nontemporal(size, matmul_rows));
   if (!fn) return hipErrorNotSupported;
-  hipLaunchKernelGGL(fn,
-                     dim3(static_cast<unsigned>(items)), dim3(cfg.threads), 0, stream, normalized, input,
-                     weight, softmax, logits, product, matrix, size, rms_rows, softmax_rows, matmul_rows, eps);
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(items)), dim3(cfg.threads), 0, stream, normalized, input,
+                     weight, softmax, logits, product, matrix, size, rms_rows, softmax_rows, matmul_rows,
+                     pair ? 1 : 0, eps);
   L2C_LAUNCH_CHECK();
   return hipSuccess;
 }
@@ -391,6 +428,10 @@ extern "C" int l2c_launch_shape(int op, int batch, int cols, int rows, int varia
         fn = reinterpret_cast<const void *>(matvec_naive_kernel);
         *grid = (rows + 63) / 64;
         *block = 64;
+      } else if (variant == L2C_MATVEC_COALESCED && pair_rows(cols, cols % 4 == 0)) {
+        fn = reinterpret_cast<const void *>(matvec_pair_kernel<true>);
+        *grid = (rows + kMatvecWaves / 2 - 1) / (kMatvecWaves / 2);
+        *block = kMatvecWaves * L2C_WAVE;
       } else if (variant == L2C_MATVEC_COALESCED) {
         fn = cols % 4 == 0 ? reinterpret_cast<const void *>(matvec_wave_kernel<true, true>)
                            : reinterpret_cast<const void *>(matvec_wave_kernel<false, true>);
@@ -403,7 +444,7 @@ extern "C" int l2c_launch_shape(int op, int batch, int cols, int rows, int varia
     case L2C_OP_FUSED: {
       const RowConfig cfg = choose_row_config(cols);
       fn = reinterpret_cast<const void *>(fused_fn(cfg, cols % 4 == 0, matvec_nontemporal(cols, rows)));
-      const long long items = fused_items(cfg, batch, batch, rows);
+      const long long items = fused_items(cfg, pair_rows(cols, cols % 4 == 0), batch, batch, rows);
       if (!fn || items > 0x7fffffffLL) return hipErrorInvalidValue;
       *grid = static_cast<int>(items);
       *block = cfg.threads;

@@ -98,8 +98,8 @@ def test_large_logits_range(torch_gpu, l2c, orc):
     assert np.all(np.isfinite(got)) and np.all(got >= 0)
 
 
-MATVEC_SHAPES = [(288, 288), (4096, 11008), (768, 2048), (1000, 300), (1001, 77), (16384, 257), (16388, 20), (32768, 33),
-                 (1, 5), (7, 1)]
+MATVEC_SHAPES = [(288, 288), (4096, 11008), (768, 2048), (1000, 300), (1001, 77), (8188, 9), (8192, 5),
+                 (8196, 9), (16384, 257), (16388, 20), (32768, 33), (1, 5), (7, 1)]
 
 
 @pytest.mark.parametrize("cols,rows", MATVEC_SHAPES)
@@ -171,7 +171,7 @@ def test_fused_partial_items(torch_gpu, l2c, orc):
 
 @pytest.mark.parametrize("batch,size,rows", [
     (8, 768, 2048), (1, 4096, 11008), (4, 16384, 1024), (1024, 16384, 64), (5, 16384, 7),
-    (3, 16388, 50), (2, 32768, 64), (2, 65536, 64), (1, 70000, 9), (2, 16385, 10), (33, 1001, 77),
+    (3, 16388, 50), (2, 8196, 11), (2, 8192, 7), (2, 32768, 64), (2, 65536, 64), (1, 70000, 9), (2, 16385, 10), (33, 1001, 77),
     (3, 1, 5)])
 def test_fused_equals_separate_launches(torch_gpu, l2c, orc, batch, size, rows):
     """The fused launch runs the row kernels' and the coalesced product's own code
@@ -200,14 +200,16 @@ def test_fused_equals_separate_launches(torch_gpu, l2c, orc, batch, size, rows):
 def test_fused_launch_shape_every_row_size(torch_gpu, l2c):
     """Every row size maps to a fused kernel instance of the row kernels' size,
     and the launch takes one workgroup per rmsnorm and softmax row plus one per
-    lanes / 64 matrix rows."""
+    lanes / 64 matrix rows (lanes / 128 for aligned rows of >= 8192 floats,
+    whose matrix rows take a pair of wavefronts)."""
     sizes = list(range(1, 300)) + [767, 768, 1000, 1001, 4095, 4096, 4097, 8192, 8196, 16380, 16384,
                                    16388, 20000, 32768, 32772, 65536, 65537, 70000, 100000]
     for size in sizes:
         grid, block, per_cu = l2c.launch_shape(l2c.OP_FUSED, 3, size, 1000)
         rgrid, rblock, _ = l2c.launch_shape(l2c.OP_RMSNORM, 3, size, 1)
         assert block == rblock, (size, block, rblock)
-        assert grid == 6 + -(-1000 // (block // 64)), (size, grid, block)
+        per_block = block // 64 // (2 if size % 4 == 0 and size >= 8192 else 1)
+        assert grid == 6 + -(-1000 // per_block), (size, grid, block)
         assert per_cu >= 1, size
 
 
