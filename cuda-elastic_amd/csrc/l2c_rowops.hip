@@ -47,10 +47,15 @@ using l2c::Row;
 
 constexpr int kMaxRowThreads = 1024;
 constexpr int kGenericThreads = 256;
-// Aligned matrices with at least this many columns are multiplied a row per
-// pair of wavefronts (l2c::matvec_pair_row); narrower ones a row per
-// wavefront (l2c::matvec_wave_row).
+// Aligned matrices with at least kPairCols columns, or at least kPairMinCols
+// columns and more than kPairBytes, are multiplied a row per pair of
+// wavefronts (l2c::matvec_pair_row); the rest a row per wavefront
+// (l2c::matvec_wave_row). Small matrices of 4096-column rows run faster a row
+// per wavefront (4096 x 4096: 10.0 against 10.4 us), large ones a row per
+// pair (4096 x 11008: 25.2 against 25.6 us).
 constexpr int kPairCols = 8192;
+constexpr int kPairMinCols = 4096;
+constexpr unsigned long long kPairBytes = 128ULL << 20;
 
 // ---------------------------------------------------------------------------
 // Kernels. V == 0 selects the two-pass generic path; MAXT is the launch
@@ -177,8 +182,12 @@ __global__ __launch_bounds__(kMatvecWaves * L2C_WAVE) void matvec_pair_kernel(
 }
 
 // The coalesced product's form: a pair of wavefronts per row for aligned rows
-// of >= kPairCols floats, else one wavefront per row.
-bool pair_rows(int cols, bool vec) { return vec && cols >= kPairCols; }
+// of >= kPairCols floats, or of >= kPairMinCols floats in a matrix of more
+// than kPairBytes; else one wavefront per row.
+bool pair_rows(int cols, int rows, bool vec) {
+  const unsigned long long w_bytes = 4ULL * static_cast<unsigned long long>(rows) * cols;
+  return vec && (cols >= kPairCols || (cols >= kPairMinCols && w_bytes > kPairBytes));
+}
 
 // Nontemporal matrix loads, except for a matrix of 128-256 MiB, which the
 // 256 MB MALL keeps between launches when it is read with ordinary loads.
@@ -357,9 +366,9 @@ extern "C" int l2c_matvec(float *out, const float *x, const float *W, int cols, 
     const bool vec = cols % 4 == 0 && l2c_aligned16(x) && l2c_aligned16(W);
     const dim3 grid((rows + kMatvecWaves - 1) / kMatvecWaves), block(kMatvecWaves * L2C_WAVE);
     const dim3 pair_grid((rows + kMatvecWaves / 2 - 1) / (kMatvecWaves / 2));
-    if (pair_rows(cols, vec) && !matvec_nontemporal(cols, rows))
+    if (pair_rows(cols, rows, vec) && !matvec_nontemporal(cols, rows))
       hipLaunchKernelGGL(matvec_pair_kernel<false>, pair_grid, block, 0, stream, out, x, W, cols, rows);
-    else if (pair_rows(cols, vec))
+    else if (pair_rows(cols, rows, vec))
       hipLaunchKernelGGL(matvec_pair_kernel<true>, pair_grid, block, 0, stream, out, x, W, cols, rows);
     else if (vec && !matvec_nontemporal(cols, rows))
       hipLaunchKernelGGL((matvec_wave_kernel<true, false>), grid, block, 0, stream, out, x, W, cols, rows);
@@ -384,7 +393,7 @@ extern "C" int l2c_fused(float *normalized, const float *input, const float *wei
   auto ok = [](const void *p) { return p == nullptr || l2c_aligned16(p); };
   const bool vec = size % 4 == 0 && ok(normalized) && ok(input) && ok(weight) && ok(softmax) &&
                    ok(logits) && ok(matrix);
-  const bool pair = pair_rows(size, vec);
+  const bool pair = pair_rows(size, matmul_rows, vec);
   const long long items = fused_items(cfg, pair, rms_rows, softmax_rows, matmul_rows);
   if (items == 0) return hipSuccess;
   if (items > 0x7fffffffLL) return hipErrorInvalidValue;
@@ -428,7 +437,7 @@ extern "C" int l2c_launch_shape(int op, int batch, int cols, int rows, int varia
         fn = reinterpret_cast<const void *>(matvec_naive_kernel);
         *grid = (rows + 63) / 64;
         *block = 64;
-      } else if (variant == L2C_MATVEC_COALESCED && pair_rows(cols, cols % 4 == 0)) {
+      } else if (variant == L2C_MATVEC_COALESCED && pair_rows(cols, rows, cols % 4 == 0)) {
         fn = reinterpret_cast<const void *>(matvec_pair_kernel<true>);
         *grid = (rows + kMatvecWaves / 2 - 1) / (kMatvecWaves / 2);
         *block = kMatvecWaves * L2C_WAVE;
@@ -444,7 +453,7 @@ extern "C" int l2c_launch_shape(int op, int batch, int cols, int rows, int varia
     case L2C_OP_FUSED: {
       const RowConfig cfg = choose_row_config(cols);
       fn = reinterpret_cast<const void *>(fused_fn(cfg, cols % 4 == 0, matvec_nontemporal(cols, rows)));
-      const long long items = fused_items(cfg, pair_rows(cols, cols % 4 == 0), batch, batch, rows);
+      const long long items = fused_items(cfg, pair_rows(cols, rows, cols % 4 == 0), batch, batch, rows);
       if (!fn || items > 0x7fffffffLL) return hipErrorInvalidValue;
       *grid = static_cast<int>(items);
       *block = cfg.threads;

@@ -99,7 +99,7 @@ def test_large_logits_range(torch_gpu, l2c, orc):
 
 
 MATVEC_SHAPES = [(288, 288), (4096, 11008), (768, 2048), (1000, 300), (1001, 77), (8188, 9), (8192, 5),
-                 (8196, 9), (16384, 257), (16388, 20), (32768, 33), (1, 5), (7, 1)]
+                 (8196, 9), (16384, 257), (16388, 20), (32768, 33), (4100, 16384), (1, 5), (7, 1)]
 
 
 @pytest.mark.parametrize("cols,rows", MATVEC_SHAPES)
@@ -201,7 +201,8 @@ def test_fused_launch_shape_every_row_size(torch_gpu, l2c):
     """Every row size maps to a fused kernel instance of the row kernels' size,
     and the launch takes one workgroup per rmsnorm and softmax row plus one per
     lanes / 64 matrix rows (lanes / 128 for aligned rows of >= 8192 floats,
-    whose matrix rows take a pair of wavefronts)."""
+    or of >= 4096 floats in a matrix of more than 128 MiB, whose matrix rows
+    take a pair of wavefronts)."""
     sizes = list(range(1, 300)) + [767, 768, 1000, 1001, 4095, 4096, 4097, 8192, 8196, 16380, 16384,
                                    16388, 20000, 32768, 32772, 65536, 65537, 70000, 100000]
     for size in sizes:
@@ -211,6 +212,11 @@ def test_fused_launch_shape_every_row_size(torch_gpu, l2c):
         per_block = block // 64 // (2 if size % 4 == 0 and size >= 8192 else 1)
         assert grid == 6 + -(-1000 // per_block), (size, grid, block)
         assert per_cu >= 1, size
+    for size, rows in [(4096, 8192), (4096, 8193), (4096, 11008), (4092, 11008), (4100, 16384), (6144, 16384),
+                       (8188, 4097), (8192, 10)]:
+        grid, block, _ = l2c.launch_shape(l2c.OP_FUSED, 3, size, rows)
+        pair = size % 4 == 0 and (size >= 8192 or (size >= 4096 and 4 * size * rows > 128 << 20))
+        assert grid == 6 + -(-rows // (block // 64 // (2 if pair else 1))), (size, rows, grid, block)
 
 
 @pytest.mark.parametrize("size", [16384, 16388, 70000])
