@@ -11,7 +11,10 @@ large shape, the fused single launch, the MXFP4 / fp8 weights on the bf16
 matrix cores and on the block-scaled fp8 matrix cores (MXFP8 activations), and the
 loom-private llama2c decoder application at its large shape, and the lowprec
 classifier experiment's fp32 / bf16 / MXFP6 / NVFP4 cases at that shape) and
-the graph/direct and copy/nocopy splits are reported under "lines".
+the graph/direct and copy/nocopy splits are each printed in full to stderr as
+a "[bench-line] {...}" JSON line; the stdout line carries only their
+microseconds ("lines") and the kernels' roofline fractions ("kernel_fracs"),
+which keeps it within MAX_STDOUT_LINE characters.
 
 The harness runs in this process (libl2c_host.so via ctypes): HIP events on
 each operation's own stream time the kernels, so `roofline` comes from the
@@ -36,6 +39,9 @@ WARMUP_MS = 100  # the reference harness's default warm-up time (llama2c_cuda_gr
 FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_f32_mfma_c4_traffic.json")
+# The result line's length bound: the driver that reads it keeps the last
+# 8,000 characters of stdout.
+MAX_STDOUT_LINE = 7500
 
 
 def log(*a):
@@ -230,6 +236,115 @@ def reference_validate_all(inp, normalized, softmax, product, batch, size, rows)
                        f"fp32 outputs, one call, one thread")}
 
 
+B_C4, S_C4, R_C4 = 1024, 16384, 8192
+
+
+def plan_args(mode, launches, batch, size, rows, copies, matmul, inputs="scaled=1", warm=100, extra=()):
+    """The harness argv of one bench line (the reference CLI's positional
+    order, llama2c_cuda_graph.cu:195-258, plus this build's keyword tokens)."""
+    return [mode, launches, batch, size, rows, 1, WARMUP_MS, copies, matmul, inputs,
+            f"warmup_iters={warm}", *extra]
+
+
+def full_plan(K, W):
+    """(name, argv) of every harness line after the headline: the graph /
+    direct and copy / nocopy splits of C2, C3 and C4, the fused launch, the
+    one-stream and host-write iteration forms, and the four C5 formats."""
+    B, S, R = B_C4, S_C4, R_C4
+    c2 = (1, 4096, 11008)
+    c3 = (8, 768, 2048)
+
+    def cfg(mode, launches, shape, copies, matmul, inputs="scaled=1", warm=W, extra=()):
+        return plan_args(mode, launches, *shape, copies, matmul, inputs=inputs, warm=warm, extra=extra)
+
+    c4 = (B, S, R)
+    plan = [
+        ("c4_batched_direct_nocopy", cfg("direct", K, c4, "nocopy", "batched")),
+        ("c4_batched_graph_copy", cfg("graph", K, c4, "copy", "batched")),
+        ("c4_batched_direct_copy", cfg("direct", K, c4, "copy", "batched")),
+        ("c4_gemv_graph_nocopy", cfg("graph", 200, c4, "nocopy", "coalesced")),
+        ("c4_gemv_direct_nocopy", cfg("direct", 200, c4, "nocopy", "coalesced")),
+        ("c4_fused_graph_nocopy", cfg("graph", 200, c4, "nocopy", "fused")),
+        ("c4_fused_direct_nocopy", cfg("direct", 200, c4, "nocopy", "fused")),
+        ("c2_gemv_graph_nocopy", cfg("graph", 1000, c2, "nocopy", "coalesced", warm=50)),
+        ("c2_gemv_direct_nocopy", cfg("direct", 1000, c2, "nocopy", "coalesced", warm=50)),
+        ("c2_fused_graph_nocopy", cfg("graph", 1000, c2, "nocopy", "fused", warm=50)),
+        ("c2_fused_direct_nocopy", cfg("direct", 1000, c2, "nocopy", "fused", warm=50)),
+        ("c3_graph_nocopy", cfg("graph", 10000, c3, "nocopy", "coalesced", warm=100)),
+        ("c3_direct_nocopy", cfg("direct", 10000, c3, "nocopy", "coalesced", warm=100)),
+        ("c3_graph_copy", cfg("graph", 10000, c3, "copy", "coalesced", warm=100)),
+        ("c3_direct_copy", cfg("direct", 10000, c3, "copy", "coalesced", warm=100)),
+        ("c3_fused_graph_nocopy", cfg("graph", 10000, c3, "nocopy", "fused", warm=100)),
+        ("c3_fused_direct_nocopy", cfg("direct", 10000, c3, "nocopy", "fused", warm=100)),
+        ("c3_fused_direct_copy", cfg("direct", 10000, c3, "copy", "fused", warm=100)),
+    ]
+    # Iteration forms beyond the reference protocol: one stream without
+    # fork/join events, and copy-mode downloads by device stores into the
+    # pinned host buffers (hostwrite) in place of memcpy nodes / calls.
+    plan += [
+        ("c3_onestream_graph_nocopy", cfg("graph", 10000, c3, "nocopy", "coalesced", warm=100, extra=("onestream",))),
+        ("c3_onestream_direct_nocopy", cfg("direct", 10000, c3, "nocopy", "coalesced", warm=100,
+                                           extra=("onestream",))),
+        ("c3_onestream_graph_copy", cfg("graph", 10000, c3, "copy", "coalesced", warm=100, extra=("onestream",))),
+        ("c3_graph_copy_hostwrite", cfg("graph", 10000, c3, "copy", "coalesced", warm=100, extra=("hostwrite",))),
+        ("c3_direct_copy_hostwrite", cfg("direct", 10000, c3, "copy", "coalesced", warm=100, extra=("hostwrite",))),
+        ("c2_onestream_graph_nocopy", cfg("graph", 1000, c2, "nocopy", "coalesced", warm=50, extra=("onestream",))),
+        ("c2_onestream_direct_nocopy", cfg("direct", 1000, c2, "nocopy", "coalesced", warm=50, extra=("onestream",))),
+        ("c4_batched_graph_copy_hostwrite", cfg("graph", K, c4, "copy", "batched", extra=("hostwrite",))),
+        ("c4_batched_direct_copy_hostwrite", cfg("direct", K, c4, "copy", "batched", extra=("hostwrite",))),
+        ("c4_batched_onestream_graph_nocopy", cfg("graph", K, c4, "nocopy", "batched", extra=("onestream",))),
+    ]
+    for fmt in ("mxfp4", "fp8", "mxfp4s", "fp8s"):
+        for mode in ("graph", "direct"):
+            for copies in ("nocopy", "copy"):
+                plan.append((f"c5_{fmt}_{mode}_{copies}", cfg(mode, K, c4, copies, fmt, inputs="normal=1")))
+        plan.append((f"c5_{fmt}_onestream_graph_nocopy",
+                     cfg("graph", K, c4, "nocopy", fmt, inputs="normal=1", extra=("onestream",))))
+    return plan
+
+
+def emit(line):
+    """Prints one bench line in full to stderr, as its own short JSON line,
+    and returns it; stdout carries only the compact summary of all lines."""
+    log("[bench-line] " + json.dumps(line, separators=(",", ":")))
+    return line
+
+
+def line_us(line):
+    """The microseconds a line is summarized by on stdout: the iteration for
+    harness lines, the compute scope per invocation for the decoder and the
+    application scope per invocation for lowprec lines."""
+    if "us_per_iter" in line:
+        return line["us_per_iter"]
+    if line["name"].startswith("lowprec_"):
+        return line["application_us_per_invocation"]
+    return line["compute_us_per_invocation"]
+
+
+def kernel_fractions(lines):
+    """Roofline fractions of each kernel, from the first line that times it
+    alone: rmsnorm / softmax / matrix-vector product against 8 TB/s of HBM,
+    the fp32 contraction against 157.3 TF, the exact C5 contractions against
+    2.5 PF bf16 and the block-scaled ones against 5.0 PF fp8."""
+    pick = {
+        "rmsnorm_c4": ("c4_batched_graph_nocopy", "rms_hbm_frac"),
+        "softmax_c4": ("c4_batched_graph_nocopy", "softmax_hbm_frac"),
+        "gemm_f32_c4": ("c4_batched_graph_nocopy", "matmul_frac"),
+        "gemv_c4": ("c4_gemv_graph_nocopy", "matmul_frac"),
+        "gemv_c2": ("c2_gemv_graph_nocopy", "matmul_frac"),
+        "qgemm_mxfp4_c5": ("c5_mxfp4_graph_nocopy", "matmul_frac"),
+        "qgemm_fp8_c5": ("c5_fp8_graph_nocopy", "matmul_frac"),
+        "scgemm_mxfp4s_c5": ("c5_mxfp4s_graph_nocopy", "matmul_frac"),
+        "scgemm_fp8s_c5": ("c5_fp8s_graph_nocopy", "matmul_frac"),
+    }
+    by_name = {ln["name"]: ln for ln in lines}
+    out = {}
+    for key, (name, field) in pick.items():
+        if name in by_name and by_name[name].get(field) is not None:
+            out[key] = round(by_name[name][field], 4)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -252,70 +367,17 @@ def main():
 
     l2c.load_host()
     K, W = args.steps, args.warmup
-    B, S, R = 1024, 16384, 8192
+    B, S, R = B_C4, S_C4, R_C4
 
-    def cfg(mode, launches, batch, size, rows, copies, matmul, inputs="scaled=1", warm=W, extra=()):
-        return [mode, launches, batch, size, rows, 1, WARMUP_MS, copies, matmul, inputs,
-                f"warmup_iters={warm}", *extra]
-
-    headline = run_line(l2c, cfg("graph", K, B, S, R, "nocopy", "batched"))
-    lines = [summarize("c4_batched_graph_nocopy", headline)]
+    headline = run_line(l2c, plan_args("graph", K, B, S, R, "nocopy", "batched", warm=W))
+    lines = [emit(summarize("c4_batched_graph_nocopy", headline))]
     if not args.quick:
-        plan = [
-            ("c4_batched_direct_nocopy", cfg("direct", K, B, S, R, "nocopy", "batched")),
-            ("c4_batched_graph_copy", cfg("graph", K, B, S, R, "copy", "batched")),
-            ("c4_batched_direct_copy", cfg("direct", K, B, S, R, "copy", "batched")),
-            ("c4_gemv_graph_nocopy", cfg("graph", 200, B, S, R, "nocopy", "coalesced")),
-            ("c4_gemv_direct_nocopy", cfg("direct", 200, B, S, R, "nocopy", "coalesced")),
-            ("c4_fused_graph_nocopy", cfg("graph", 200, B, S, R, "nocopy", "fused")),
-            ("c4_fused_direct_nocopy", cfg("direct", 200, B, S, R, "nocopy", "fused")),
-            ("c2_gemv_graph_nocopy", cfg("graph", 1000, 1, 4096, 11008, "nocopy", "coalesced", warm=50)),
-            ("c2_gemv_direct_nocopy", cfg("direct", 1000, 1, 4096, 11008, "nocopy", "coalesced", warm=50)),
-            ("c2_fused_graph_nocopy", cfg("graph", 1000, 1, 4096, 11008, "nocopy", "fused", warm=50)),
-            ("c2_fused_direct_nocopy", cfg("direct", 1000, 1, 4096, 11008, "nocopy", "fused", warm=50)),
-            ("c3_graph_nocopy", cfg("graph", 10000, 8, 768, 2048, "nocopy", "coalesced", warm=100)),
-            ("c3_direct_nocopy", cfg("direct", 10000, 8, 768, 2048, "nocopy", "coalesced", warm=100)),
-            ("c3_graph_copy", cfg("graph", 10000, 8, 768, 2048, "copy", "coalesced", warm=100)),
-            ("c3_direct_copy", cfg("direct", 10000, 8, 768, 2048, "copy", "coalesced", warm=100)),
-            ("c3_fused_graph_nocopy", cfg("graph", 10000, 8, 768, 2048, "nocopy", "fused", warm=100)),
-            ("c3_fused_direct_nocopy", cfg("direct", 10000, 8, 768, 2048, "nocopy", "fused", warm=100)),
-            ("c3_fused_direct_copy", cfg("direct", 10000, 8, 768, 2048, "copy", "fused", warm=100)),
-        ]
-        # Iteration forms beyond the reference protocol: one stream without
-        # fork/join events, and copy-mode downloads by device stores into the
-        # pinned host buffers (hostwrite) in place of memcpy nodes / calls.
-        plan += [
-            ("c3_onestream_graph_nocopy", cfg("graph", 10000, 8, 768, 2048, "nocopy", "coalesced", warm=100,
-                                              extra=("onestream",))),
-            ("c3_onestream_direct_nocopy", cfg("direct", 10000, 8, 768, 2048, "nocopy", "coalesced", warm=100,
-                                               extra=("onestream",))),
-            ("c3_onestream_graph_copy", cfg("graph", 10000, 8, 768, 2048, "copy", "coalesced", warm=100,
-                                            extra=("onestream",))),
-            ("c3_graph_copy_hostwrite", cfg("graph", 10000, 8, 768, 2048, "copy", "coalesced", warm=100,
-                                            extra=("hostwrite",))),
-            ("c3_direct_copy_hostwrite", cfg("direct", 10000, 8, 768, 2048, "copy", "coalesced", warm=100,
-                                             extra=("hostwrite",))),
-            ("c2_onestream_graph_nocopy", cfg("graph", 1000, 1, 4096, 11008, "nocopy", "coalesced", warm=50,
-                                              extra=("onestream",))),
-            ("c2_onestream_direct_nocopy", cfg("direct", 1000, 1, 4096, 11008, "nocopy", "coalesced", warm=50,
-                                               extra=("onestream",))),
-            ("c4_batched_graph_copy_hostwrite", cfg("graph", K, B, S, R, "copy", "batched", extra=("hostwrite",))),
-            ("c4_batched_direct_copy_hostwrite", cfg("direct", K, B, S, R, "copy", "batched", extra=("hostwrite",))),
-            ("c4_batched_onestream_graph_nocopy", cfg("graph", K, B, S, R, "nocopy", "batched", extra=("onestream",))),
-        ]
-        for fmt in ("mxfp4", "fp8", "mxfp4s", "fp8s"):
-            for mode in ("graph", "direct"):
-                for copies in ("nocopy", "copy"):
-                    plan.append((f"c5_{fmt}_{mode}_{copies}",
-                                 cfg(mode, K, B, S, R, copies, fmt, inputs="normal=1")))
-            plan.append((f"c5_{fmt}_onestream_graph_nocopy",
-                         cfg("graph", K, B, S, R, "nocopy", fmt, inputs="normal=1", extra=("onestream",))))
-        for name, a in plan:
-            lines.append(summarize(name, run_line(l2c, a)))
+        for name, a in full_plan(K, W):
+            lines.append(emit(summarize(name, run_line(l2c, a))))
         for mode in ("graph", "direct"):
-            lines.append(decoder_line(l2c, mode))
+            lines.append(emit(decoder_line(l2c, mode)))
         for case in ("fp32", "bf16", "mxfp6", "nvfp4"):
-            lines.append(lowprec_line(l2c, case))
+            lines.append(emit(lowprec_line(l2c, case)))
 
     gemm_us = headline["matmul_us"]
     flops = 2.0 * B * R * S
@@ -364,10 +426,21 @@ def main():
         "rms_gbps": headline["rms_gbps"], "softmax_gbps": headline["softmax_gbps"],
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "lines": lines,
+        # Every line in full is on stderr ("[bench-line] {...}"); here only its
+        # microseconds (iteration, or invocation for decoder / lowprec lines)
+        # and each kernel's roofline fraction, so the line stays short.
+        "lines": {ln["name"]: round(line_us(ln), 2) for ln in lines},
+        "kernel_fracs": kernel_fractions(lines),
         "device": headline.get("device"),
     }
-    print(json.dumps(result), flush=True)
+    text = json.dumps(result)
+    if len(text) > MAX_STDOUT_LINE:
+        # Keep the headline, roofline and cpu baseline readable: the per-line
+        # microseconds are on stderr anyway.
+        log(f"[bench] WARNING: result line of {len(text)} characters; dropping the lines map from stdout")
+        result["lines"] = {"c4_batched_graph_nocopy": result["lines"]["c4_batched_graph_nocopy"]}
+        text = json.dumps(result)
+    print(text, flush=True)
     return 0
 
 
