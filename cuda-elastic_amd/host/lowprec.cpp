@@ -1,80 +1,289 @@
-// The lowprec decoder classifier experiment on MI355X: the llama2c decoder
-// (loom-private/llama2c-decoder) with only its dense classifier replaced by
-// a BF16, MXFP6 or NVFP4 contraction, under the loom_private protocol, plus
-// the specification's self-test and accuracy modes.
+// The lowprec classifier experiment on MI355X (experiments/blackwell/lowprec):
+// the llama2c decoder of loom-private/llama2c-decoder with only its dense
+// classifier replaced, case by case, by a BF16, MXFP6 or NVFP4 contraction, or
+// kept in FP32 (the control). Three modes:
+//   the loom_private protocol   check / bench / profile (app_protocol.h)
+//   --selftest                  the device conversion of a crafted matrix
+//                               against the host quantizer
+//   --accuracy                  numerical quality on the primary model and
+//                               the three dense fixtures
 //
-// What it must do is fixed by experiments/blackwell/lowprec (spec.json: cases,
-// formats, checks, metrics; decoder_lowprec.cu: the workload, its checks and
-// modes; README.md). Per step: l2c_decoder_rmsnorm -> the case's activation
-// conversion -> the case's classifier -> l2c_decoder_softmax_argmax with the
-// token fed back on the device. Weights are converted once at setup.
-//   fp32   l2c_matmul (the decoder's classifier, fp32 matrix cores)
-//   bf16   l2c_to_bf16_x4 -> l2c_matmul_bf16
-//   mxfp6  l2c_quantize_mxfp6 -> l2c_matmul_mxfp6 (scaled matrix cores)
-//   nvfp4  l2c_nvfp4_tensor_scales (s, d, alpha) -> l2c_quantize_nvfp4 (codes,
-//          scales and the exact bf16 expansion) -> l2c_matmul_bf16 with alpha
-//          read from device memory
+// Parts of this file:
+//   HostModel             what the host knows of the model the GPU runs
+//   ClassifierExperiment  the application: device state, the per-step
+//                         enqueue, and host snapshots of an invocation
+//   Stage, Audit          the implementation check, one stage at a time
+//   Assessment            one dataset of --accuracy
+// Formats and their device planes are in lowprec_formats.h; the host
+// quantizer, fixtures and double references in lowprec_reference.h.
+//
+// What callers rely on (option names, exit codes, the record schemas and
+// scope strings, the dimension messages) follows spec.json and the
+// reference's tests/run_tests.sh; the organisation is this build's own.
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <mutex>
+#include <numeric>
 #include <string>
 #include <thread>
 #include <vector>
 
 #include "../../include/l2c.h"
 #include "../../include/l2c_harness.h"
-#include "decoder_contract.h"
-#include "lowprec_reference.h"
 #include "app_protocol.h"
+#include "decoder_contract.h"
+#include "lowprec_formats.h"
+#include "lowprec_reference.h"
 #include "parallel.h"
 
 namespace {
 
+using appproto::Json;
 using l2c_decoder::DeviceArray;
 using l2c_decoder::device_array;
+using l2c_decoder::Dims;
 using l2c_decoder::PinnedArray;
 using l2c_decoder::pinned_array;
 using namespace lowprec;
 
-constexpr long long kLargeBatch = 1024, kLargeWidth = 16384, kLargeVocab = 8192, kLargeSteps = 4;
-constexpr long long kFixtureBatch = 64, kFixtureWidth = 1024, kFixtureVocab = 128;
+// The experiment's two shapes (spec.json "dimensions").
+constexpr Dims kPrimary{1024, 16384, 8192, 4};
+constexpr Dims kFixtureShape{64, 1024, 128, 4};
 constexpr double kDeviceLimitGiB = 64.0;
-// sha256 of experiments/blackwell/lowprec/spec.json, the specification this
-// application implements (recorded in every result).
+// sha256 of experiments/blackwell/lowprec/spec.json, recorded in every result.
 constexpr const char *kSpecSha256 = "1a56ed12366829cbf1b952d99267143f4d74f64411858cb6e7748e389616a64c";
-constexpr int kReportLimit = 5;
+constexpr const char kProgram[] = "decoder_lowprec";
+// Failures printed per check stage before the rest are only counted.
+constexpr long long kShownPerStage = 5;
 
-int threads() { return static_cast<int>(std::max(1u, std::min(16u, std::thread::hardware_concurrency()))); }
+int host_threads() {
+  return static_cast<int>(std::max(1u, std::min(16u, std::thread::hardware_concurrency())));
+}
 
-// The converted form of one [rows][width] operand on the device.
-struct Operand {
-  long long rows = 0, width = 0;
-  DeviceArray<uint8_t> codes;    // MXFP6: 3 bytes per 4 values; NVFP4: 1 per 2
-  DeviceArray<uint8_t> scales;   // one byte per block, [rows][width / block]
-  DeviceArray<uint16_t> wide;    // bf16 values (BF16) or the NVFP4 bf16 expansion
-  DeviceArray<float> tensor;     // NVFP4: s, d
-  size_t code_bytes = 0, scale_bytes = 0, wide_count = 0;
+// f(i) for i in [0, n) over the host threads, in contiguous ranges.
+template <typename F>
+void spread(long long n, F f) {
+  l2c_host::parallel_ranges(static_cast<size_t>(n), host_threads(), [&](size_t i0, size_t i1, size_t) {
+    for (size_t i = i0; i < i1; ++i) f(static_cast<long long>(i));
+  });
+}
+
+std::string identity(int c) { return std::string("blackwell-experiments/lowprec-decoder-classifier/") + case_name(c); }
+
+// ---------------------------------------------------------------------------
+// HostModel: the primary (synthetic) model or a dense fixture, as the host
+// evaluates it. The synthetic model is never materialized on the host except
+// where a caller asks for the whole classifier.
+
+class HostModel {
+ public:
+  static HostModel synthetic(long long width, long long vocab) { return HostModel(0, width, vocab); }
+  static HostModel dense(int seed, long long width, long long vocab) {
+    HostModel m(seed, width, vocab);
+    const size_t n = static_cast<size_t>(width * vocab);
+    m.embedding_.resize(n);
+    m.classifier_.resize(n);
+    fixture(seed, width, vocab, m.embedding_.data(), m.classifier_.data());
+    return m;
+  }
+
+  int seed() const { return seed_; }
+  bool is_synthetic() const { return seed_ == 0; }
+  long long width() const { return width_; }
+  long long vocab() const { return vocab_; }
+  long long prompt(long long sequence) const { return sequence % vocab_; }
+
+  // Embedding row of a token; the synthetic row (1, and 4 at the token's own
+  // column) is written into *scratch.
+  const float *embedding_row(long long token, std::vector<float> *scratch) const {
+    if (!is_synthetic()) return &embedding_[static_cast<size_t>(token * width_)];
+    scratch->assign(static_cast<size_t>(width_), 1.0f);
+    (*scratch)[static_cast<size_t>(token)] = 4.0f;
+    return scratch->data();
+  }
+
+  // The classifier's only nonzero column in row r of the synthetic model.
+  long long synthetic_column(long long r) const { return (r + vocab_ - 1) % vocab_; }
+
+  // The whole classifier, [vocab][width] floats.
+  std::vector<float> classifier() const {
+    if (!is_synthetic()) return classifier_;
+    std::vector<float> w(static_cast<size_t>(vocab_ * width_), 0.0f);
+    for (long long r = 0; r < vocab_; ++r) w[static_cast<size_t>(r * width_ + synthetic_column(r))] = 1.0f;
+    return w;
+  }
+
+  // Logit r of activations x: the double dot product with classifier row r.
+  double logit(const float *x, long long r) const {
+    if (is_synthetic()) return x[synthetic_column(r)];
+    const float *w = &classifier_[static_cast<size_t>(r * width_)];
+    double sum = 0.0;
+    for (long long k = 0; k < width_; ++k) sum += static_cast<double>(x[k]) * w[k];
+    return sum;
+  }
+
+  void upload(float *embedding, float *classifier, float *norm_weight, hipStream_t stream) const {
+    if (is_synthetic()) {
+      APP_L2C(l2c_decoder_init_model(embedding, classifier, norm_weight, static_cast<int>(width_),
+                                     static_cast<int>(vocab_), stream));
+      return;
+    }
+    const std::vector<float> ones(static_cast<size_t>(width_), 1.0f);
+    APP_HIP(hipMemcpyAsync(embedding, embedding_.data(), embedding_.size() * 4, hipMemcpyHostToDevice, stream));
+    APP_HIP(hipMemcpyAsync(classifier, classifier_.data(), classifier_.size() * 4, hipMemcpyHostToDevice, stream));
+    APP_HIP(hipMemcpyAsync(norm_weight, ones.data(), ones.size() * 4, hipMemcpyHostToDevice, stream));
+    APP_HIP(hipStreamSynchronize(stream));  // `ones` leaves scope
+  }
+
+  // Greedy tokens [batch][steps] in exact arithmetic: the synthetic model
+  // moves every token to its successor; a dense model is decoded on the host
+  // in double (rmsnorm, every logit, first largest).
+  std::vector<int> reference_tokens(long long batch, long long steps) const {
+    std::vector<int> out(static_cast<size_t>(batch * steps));
+    spread(batch, [&](long long b) {
+      std::vector<double> normalized(static_cast<size_t>(width_)), logits(static_cast<size_t>(vocab_));
+      std::vector<float> scratch;
+      long long token = prompt(b);
+      for (long long s = 0; s < steps; ++s) {
+        if (is_synthetic()) {
+          token = (token + 1) % vocab_;
+        } else {
+          rmsnorm_double(embedding_row(token, &scratch), width_, normalized.data());
+          for (long long r = 0; r < vocab_; ++r) {
+            const float *w = &classifier_[static_cast<size_t>(r * width_)];
+            double sum = 0.0;
+            for (long long k = 0; k < width_; ++k) sum += normalized[static_cast<size_t>(k)] * w[k];
+            logits[static_cast<size_t>(r)] = sum;
+          }
+          token = argmax_first(logits.data(), vocab_);
+        }
+        out[static_cast<size_t>(b * steps + s)] = static_cast<int>(token);
+      }
+    });
+    return out;
+  }
+
+ private:
+  HostModel(int seed, long long width, long long vocab) : seed_(seed), width_(width), vocab_(vocab) {}
+  int seed_;
+  long long width_, vocab_;
+  std::vector<float> embedding_, classifier_;
 };
 
-class LowprecWorkload final : public appproto::Application {
+// ---------------------------------------------------------------------------
+// Host copy of what one invocation left on the device.
+
+struct Snapshot {
+  std::vector<int> generated;                           // [batch][steps]
+  std::vector<float> normalized, logits, probabilities;  // [steps][batch][...]
+  std::vector<PlaneBytes> activations;                   // per step, the format's planes
+  std::vector<float> alpha;                              // NVFP4, per step
+};
+
+// The converted weights, compared once against the host quantizer.
+struct WeightReading {
+  long long values = 0, differing = 0;
+  Quantized host;                // the host quantizer's codes of the FP32 weights
+  std::vector<float> values_f;   // their values without the NVFP4 tensor scale
+};
+
+// ---------------------------------------------------------------------------
+// Stage: one stage of the implementation check. Counts compared and failed
+// items from any thread and prints the first few failures.
+
+class Stage {
  public:
-  LowprecWorkload(int lowprec_case, long long batch, long long width, long long vocab, long long steps, int fixture,
-                  int fault = 0)
-      : c_(lowprec_case), d_{batch, width, vocab, steps}, fixture_(fixture), fault_(fault) {}
+  explicit Stage(const char *name) : name_(name) {}
+  const char *name() const { return name_; }
+  void compared(long long n) { checked_ += n; }
+  void failed(const char *format, ...) __attribute__((format(printf, 2, 3))) {
+    if (failures_.fetch_add(1) >= kShownPerStage) return;
+    char line[512];
+    va_list args;
+    va_start(args, format);
+    std::vsnprintf(line, sizeof line, format, args);
+    va_end(args);
+    std::lock_guard<std::mutex> lock(print_);
+    std::fprintf(stderr, "%s: %s: %s\n", appproto::program(), name_, line);
+  }
+  // A failure already reported elsewhere (counted, not printed).
+  void failed_silently(long long n) { failures_ += n; }
+  void worst(double ratio) {
+    std::lock_guard<std::mutex> lock(print_);
+    worst_ = std::max(worst_, ratio);
+  }
+  bool ok() const { return failures_.load() == 0; }
+  long long failures() const { return failures_.load(); }
+  std::string tally() const {
+    char text[160];
+    std::snprintf(text, sizeof text, "%s %lld/%lld failed", name_, failures_.load(), checked_.load());
+    std::string out = text;
+    if (worst_ > 0.0) {
+      std::snprintf(text, sizeof text, " (largest passing error / bound %.3g)", worst_);
+      out += text;
+    }
+    return out;
+  }
+
+ private:
+  const char *name_;
+  std::atomic<long long> checked_{0}, failures_{0};
+  double worst_ = 0.0;
+  std::mutex print_;
+};
+
+// Codes, scales and the NVFP4 decode scale of `device` against `host`, the
+// same [rows][width] operand; the differences go to `stage`.
+void match_codes(Stage &stage, const char *what, const Quantized &host, const Quantized &device, long long width) {
+  stage.compared(static_cast<long long>(host.codes.size() + host.scales.size()));
+  for (size_t i = 0; i < host.codes.size(); ++i)
+    if (host.codes[i] != device.codes[i])
+      stage.failed("%s code mismatch at row %lld column %lld: host quantizer 0x%x, device 0x%x", what,
+                   static_cast<long long>(i) / width, static_cast<long long>(i) % width, host.codes[i],
+                   device.codes[i]);
+  const long long blocks_per_row = host.scales.empty() ? 1 : static_cast<long long>(host.scales.size()) /
+                                                                 (static_cast<long long>(host.codes.size()) / width);
+  for (size_t i = 0; i < host.scales.size(); ++i)
+    if (host.scales[i] != device.scales[i])
+      stage.failed("%s scale mismatch at row %lld block %lld: host quantizer 0x%02x, device 0x%02x", what,
+                   static_cast<long long>(i) / blocks_per_row, static_cast<long long>(i) % blocks_per_row,
+                   host.scales[i], device.scales[i]);
+  if (!(host.decode == device.decode))
+    stage.failed("%s tensor decode scale mismatch: host %.9g, device %.9g", what, static_cast<double>(host.decode),
+                 static_cast<double>(device.decode));
+}
+
+// ---------------------------------------------------------------------------
+// ClassifierExperiment: the decoder with the case's classifier, under the
+// loom_private protocol. Per step on one stream: rmsnorm of the current
+// tokens' embedding rows -> the case's activation conversion -> its
+// contraction -> softmax + argmax, which writes the next tokens.
+
+class ClassifierExperiment final : public appproto::Application {
+ public:
+  // Test hooks (--set fault=N, check only), planted in what the host reads
+  // back rather than in the kernels: 1 moves one step-0 activation code one
+  // step toward zero, 2 exchanges two differing neighbouring step-0 block
+  // scales, 3 divides the logits by alpha (a contraction that dropped alpha).
+  enum Fault { kNoFault = 0, kRounding = 1, kScaleLayout = 2, kAlpha = 3 };
+
+  ClassifierExperiment(int lowprec_case, const Dims &dims, HostModel model, int fault)
+      : case_(lowprec_case), d_(dims), model_(std::move(model)), fault_(fault), format_(make_format(lowprec_case)) {}
 
   appproto::AppInfo info() const override {
-    using appproto::Json;
     appproto::AppInfo i;
-    i.identity = std::string("blackwell-experiments/lowprec-decoder-classifier/") + case_name(c_);
+    i.identity = identity(case_);
     i.dimensions.add("batch", Json::whole(d_.batch))
         .add("width", Json::whole(d_.width))
         .add("vocab", Json::whole(d_.vocab))
         .add("steps", Json::whole(d_.steps))
-        .add("fixture", Json::whole(fixture_))
-        .add("case", Json::text(case_name(c_)))
+        .add("fixture", Json::whole(model_.seed()))
+        .add("case", Json::text(case_name(case_)))
         .add("generated_tokens", Json::whole(d_.batch * d_.steps))
         .add("classifier_macs_per_step", Json::whole(d_.batch * d_.vocab * d_.width));
     i.application_scope =
@@ -86,25 +295,17 @@ class LowprecWorkload final : public appproto::Application {
     return i;
   }
 
-  long long batch() const { return d_.batch; }
-  long long width() const { return d_.width; }
-  long long vocab() const { return d_.vocab; }
-  long long steps() const { return d_.steps; }
-  const std::vector<float> &host_embedding() const { return host_embedding_; }
-  const std::vector<float> &host_classifier() const { return host_classifier_; }
-  float *normalized(long long s) const { return normalized_.get() + d_.activation_at(0, s); }
-  float *logits(long long s) const { return logits_.get() + d_.row_at(0, s); }
-  const int *generated() const { return host_generated_.get(); }
-  void download_outputs(float *normalized_out, float *logits_out, float *probabilities_out) const {
-    APP_HIP(hipMemcpy(normalized_out, normalized_.get(), d_.activation_count() * 4, hipMemcpyDeviceToHost));
-    APP_HIP(hipMemcpy(logits_out, logits_.get(), d_.row_count() * 4, hipMemcpyDeviceToHost));
-    APP_HIP(hipMemcpy(probabilities_out, probabilities_.get(), d_.row_count() * 4, hipMemcpyDeviceToHost));
-  }
+  const Dims &dims() const { return d_; }
+  const HostModel &model() const { return model_; }
+  int lowprec_case() const { return case_; }
+  float *normalized(long long step) const { return normalized_.get() + d_.activation_at(0, step); }
+  float *logits(long long step) const { return logits_.get() + d_.row_at(0, step); }
+  double setup_encode_ms() const { return setup_encode_ms_; }
 
   void prepare(hipStream_t stream) override {
-    const size_t model_count = static_cast<size_t>(d_.vocab * d_.width);
-    embedding_ = device_array<float>(model_count);
-    classifier_ = device_array<float>(model_count);
+    const size_t model_values = static_cast<size_t>(d_.vocab * d_.width);
+    embedding_ = device_array<float>(model_values);
+    classifier_ = device_array<float>(model_values);
     norm_weight_ = device_array<float>(static_cast<size_t>(d_.width));
     prompts_ = device_array<int>(static_cast<size_t>(d_.batch));
     tokens_ = device_array<int>(static_cast<size_t>(d_.batch));
@@ -112,575 +313,425 @@ class LowprecWorkload final : public appproto::Application {
     normalized_ = device_array<float>(d_.activation_count());
     logits_ = device_array<float>(d_.row_count());
     probabilities_ = device_array<float>(d_.row_count());
-    partials_ = device_array<float>(L2C_NVFP4_PARTIALS);
-    host_prompts_ = pinned_array<int>(static_cast<size_t>(d_.batch));
-    host_generated_ = pinned_array<int>(d_.token_count());
-    if (fixture_ == 0) {
-      APP_L2C(l2c_decoder_init_model(embedding_.get(), classifier_.get(), norm_weight_.get(),
-                                    static_cast<int>(d_.width), static_cast<int>(d_.vocab), stream));
-    } else {
-      host_embedding_.resize(model_count);
-      host_classifier_.resize(model_count);
-      lowprec::fixture(fixture_, d_.width, d_.vocab, host_embedding_.data(), host_classifier_.data());
-      const std::vector<float> ones(static_cast<size_t>(d_.width), 1.0f);
-      APP_HIP(hipMemcpyAsync(embedding_.get(), host_embedding_.data(), model_count * 4, hipMemcpyHostToDevice, stream));
-      APP_HIP(hipMemcpyAsync(classifier_.get(), host_classifier_.data(), model_count * 4, hipMemcpyHostToDevice, stream));
-      APP_HIP(hipMemcpyAsync(norm_weight_.get(), ones.data(), ones.size() * 4, hipMemcpyHostToDevice, stream));
-      APP_HIP(hipStreamSynchronize(stream));
-    }
-    for (long long b = 0; b < d_.batch; ++b) host_prompts_.get()[b] = static_cast<int>(b % d_.vocab);
-    if (c_ != kFp32) {
-      weights_ = make_operand(d_.vocab);
-      for (long long s = 0; s < d_.steps; ++s) activations_.push_back(make_operand(d_.batch));
-      if (c_ == kNvfp4) alpha_ = device_array<float>(static_cast<size_t>(d_.steps));
-    }
-    APP_HIP(hipStreamSynchronize(stream));
-    hipEvent_t start, stop;
-    APP_HIP(hipEventCreate(&start));
-    APP_HIP(hipEventCreate(&stop));
-    APP_HIP(hipEventRecord(start, stream));
-    convert_weights(stream);
-    APP_HIP(hipEventRecord(stop, stream));
-    APP_HIP(hipEventSynchronize(stop));
+    pinned_prompts_ = pinned_array<int>(static_cast<size_t>(d_.batch));
+    pinned_generated_ = pinned_array<int>(d_.token_count());
+    for (long long b = 0; b < d_.batch; ++b) pinned_prompts_.get()[b] = static_cast<int>(model_.prompt(b));
+    model_.upload(embedding_.get(), classifier_.get(), norm_weight_.get(), stream);
+    weights_ = format_->allocate(d_.vocab, d_.width);
+    for (long long s = 0; s < d_.steps; ++s) step_inputs_.push_back(format_->allocate(d_.batch, d_.width));
+    if (case_ == kNvfp4) alpha_ = device_array<float>(static_cast<size_t>(d_.steps));
+    setup_encode_ms_ = time_ms(stream, [&] { encode_weights(stream); });
+    std::fprintf(stderr, "%s: %s classifier, %s model: weights converted in %.3f ms at setup\n", appproto::program(),
+                 case_name(case_), model_.is_synthetic() ? "synthetic" : ("fixture " + std::to_string(model_.seed())).c_str(),
+                 setup_encode_ms_);
+  }
+
+  void encode_weights(hipStream_t stream) { format_->encode(classifier_.get(), weights_, nullptr, nullptr, stream); }
+
+  // Times `work` on `stream` with a pair of events, in milliseconds.
+  template <typename F>
+  static double time_ms(hipStream_t stream, F work) {
+    hipEvent_t begin, end;
+    APP_HIP(hipEventCreate(&begin));
+    APP_HIP(hipEventCreate(&end));
+    APP_HIP(hipEventRecord(begin, stream));
+    work();
+    APP_HIP(hipEventRecord(end, stream));
+    APP_HIP(hipEventSynchronize(end));
     float ms = 0.0f;
-    APP_HIP(hipEventElapsedTime(&ms, start, stop));
-    (void)hipEventDestroy(start);
-    (void)hipEventDestroy(stop);
-    std::fprintf(stderr, "%s: case %s, fixture %d, weight conversion %.3f ms (setup)\n", appproto::program(),
-                 case_name(c_), fixture_, static_cast<double>(ms));
+    APP_HIP(hipEventElapsedTime(&ms, begin, end));
+    (void)hipEventDestroy(begin);
+    (void)hipEventDestroy(end);
+    return ms;
   }
 
   void enqueue(appproto::Scope scope, hipStream_t stream) override {
-    const bool whole = scope == appproto::Scope::kApplication;
-    if (whole)
-      APP_HIP(hipMemcpyAsync(prompts_.get(), host_prompts_.get(), static_cast<size_t>(d_.batch) * sizeof(int),
-                             hipMemcpyHostToDevice, stream));
-    enqueue_steps(stream);
-    if (whole)
-      APP_HIP(hipMemcpyAsync(host_generated_.get(), generated_.get(), d_.token_count() * sizeof(int),
-                             hipMemcpyDeviceToHost, stream));
-  }
-
-  void enqueue_steps(hipStream_t stream) {
-    APP_HIP(hipMemcpyAsync(tokens_.get(), prompts_.get(), static_cast<size_t>(d_.batch) * sizeof(int),
-                          hipMemcpyDeviceToDevice, stream));
+    const bool application = scope == appproto::Scope::kApplication;
+    const size_t token_bytes = static_cast<size_t>(d_.batch) * sizeof(int);
+    if (application)
+      APP_HIP(hipMemcpyAsync(prompts_.get(), pinned_prompts_.get(), token_bytes, hipMemcpyHostToDevice, stream));
+    APP_HIP(hipMemcpyAsync(tokens_.get(), prompts_.get(), token_bytes, hipMemcpyDeviceToDevice, stream));
     const int B = static_cast<int>(d_.batch), W = static_cast<int>(d_.width), V = static_cast<int>(d_.vocab),
               S = static_cast<int>(d_.steps);
     for (int s = 0; s < S; ++s) {
       APP_L2C(l2c_decoder_rmsnorm(normalized(s), tokens_.get(), embedding_.get(), norm_weight_.get(), W, V, B, stream));
-      enqueue_classifier(s, stream);
+      classify(s, stream);
       APP_L2C(l2c_decoder_softmax_argmax(probabilities_.get() + d_.row_at(0, s), logits(s), tokens_.get(),
-                                        generated_.get(), V, B, S, s, stream));
+                                         generated_.get(), V, B, S, s, stream));
     }
+    if (application)
+      APP_HIP(hipMemcpyAsync(pinned_generated_.get(), generated_.get(), d_.token_count() * sizeof(int),
+                             hipMemcpyDeviceToHost, stream));
   }
 
-  // The classifier of step s on whatever normalized(s) holds.
-  void enqueue_classifier(int s, hipStream_t stream) {
-    const int B = static_cast<int>(d_.batch), W = static_cast<int>(d_.width), V = static_cast<int>(d_.vocab);
-    if (c_ == kFp32) {
-      APP_L2C(l2c_matmul(logits(s), normalized(s), classifier_.get(), B, W, V, stream));
-      return;
-    }
-    Operand &a = activations_[static_cast<size_t>(s)];
-    convert(normalized(s), a, alpha_ ? alpha_.get() + s : nullptr, stream);
-    if (c_ == kMxfp6)
-      APP_L2C(l2c_matmul_mxfp6(logits(s), a.codes.get(), a.scales.get(), weights_.codes.get(), weights_.scales.get(), B,
-                              W, V, stream));
-    else
-      APP_L2C(l2c_matmul_bf16(logits(s), a.wide.get(), weights_.wide.get(), c_ == kNvfp4 ? alpha_.get() + s : nullptr,
-                             B, W, V, stream));
-  }
-
-  void convert_weights(hipStream_t stream) {
-    if (c_ != kFp32) convert(classifier_.get(), weights_, nullptr, stream);
+  // The case's classifier for one step: whatever normalized(step) holds is
+  // converted (NVFP4: with that step's alpha) and contracted with the weights.
+  void classify(long long step, hipStream_t stream) {
+    DeviceTensor &x = step_inputs_[static_cast<size_t>(step)];
+    float *alpha = alpha_ ? alpha_.get() + step : nullptr;
+    format_->encode(normalized(step), x, alpha, format_->decode_scale(weights_), stream);
+    format_->contract(logits(step), normalized(step), x, classifier_.get(), weights_, alpha,
+                      static_cast<int>(d_.batch), static_cast<int>(d_.width), static_cast<int>(d_.vocab), stream);
   }
 
   void scramble_outputs(hipStream_t stream) override {
-    auto poison = [&](void *p, size_t bytes) {
-      if (p && bytes) APP_HIP(hipMemsetAsync(p, 0xFF, bytes, stream));
-    };
-    poison(prompts_.get(), static_cast<size_t>(d_.batch) * sizeof(int));
-    poison(tokens_.get(), static_cast<size_t>(d_.batch) * sizeof(int));
-    poison(generated_.get(), d_.token_count() * sizeof(int));
-    poison(normalized_.get(), d_.activation_count() * sizeof(float));
-    poison(logits_.get(), d_.row_count() * sizeof(float));
-    poison(probabilities_.get(), d_.row_count() * sizeof(float));
-    for (Operand &a : activations_) {
-      poison(a.codes.get(), a.code_bytes);
-      poison(a.scales.get(), a.scale_bytes);
-      poison(a.wide.get(), a.wide_count * 2);
-      poison(a.tensor.get(), 8);
-    }
-    if (alpha_) poison(alpha_.get(), static_cast<size_t>(d_.steps) * 4);
-    std::memset(host_generated_.get(), 0xFF, d_.token_count() * sizeof(int));
+    const auto fill = [&](void *p, size_t bytes) { APP_HIP(hipMemsetAsync(p, 0xFF, bytes, stream)); };
+    fill(prompts_.get(), static_cast<size_t>(d_.batch) * sizeof(int));
+    fill(tokens_.get(), static_cast<size_t>(d_.batch) * sizeof(int));
+    fill(generated_.get(), d_.token_count() * sizeof(int));
+    fill(normalized_.get(), d_.activation_count() * sizeof(float));
+    fill(logits_.get(), d_.row_count() * sizeof(float));
+    fill(probabilities_.get(), d_.row_count() * sizeof(float));
+    for (const DeviceTensor &x : step_inputs_) poison(x, stream);
+    if (alpha_) fill(alpha_.get(), static_cast<size_t>(d_.steps) * sizeof(float));
+    std::memset(pinned_generated_.get(), 0xFF, d_.token_count() * sizeof(int));
   }
 
   void derive_expected() override {
-    if (c_ != kFp32) {
-      APP_HIP(hipDeviceSynchronize());
-      const std::vector<float> w = host_weights();
-      const Quantized expected = quantize(c_, w.data(), d_.vocab, d_.width);
-      const Quantized actual = download(weights_);
-      weights_match_ = compare("weights", expected, actual, d_.vocab);
-      dequantized_weights_.resize(w.size());
-      l2c_host::parallel_ranges(static_cast<size_t>(d_.vocab), threads(), [&](size_t r0, size_t r1, size_t) {
-        for (long long r = static_cast<long long>(r0); r < static_cast<long long>(r1); ++r)
-          for (long long k = 0; k < d_.width; ++k)
-            dequantized_weights_[static_cast<size_t>(r * d_.width + k)] = dequantized(c_, expected, d_.width, r, k);
-      });
-      weight_decode_ = expected.decode;
-    }
-    if (c_ == kFp32 && fixture_ == 0) contract_ = std::make_unique<l2c_decoder::Expectation>(d_);
+    APP_HIP(hipDeviceSynchronize());
+    if (case_ != kFp32) read_weights();
+    if (case_ == kFp32 && model_.is_synthetic()) production_ = std::make_unique<l2c_decoder::Expectation>(d_);
   }
 
-  bool outputs_match() override {
-    download_diagnostics();
-    if (fault_ == 3) {
-      // Logits as a contraction that ignored alpha would leave them.
-      for (float &l : host_logits_) l /= alpha_host_;
+  Snapshot snapshot() const {
+    Snapshot s;
+    s.generated.assign(pinned_generated_.get(), pinned_generated_.get() + d_.token_count());
+    s.normalized.resize(d_.activation_count());
+    s.logits.resize(d_.row_count());
+    s.probabilities.resize(d_.row_count());
+    APP_HIP(hipMemcpy(s.normalized.data(), normalized_.get(), s.normalized.size() * 4, hipMemcpyDeviceToHost));
+    APP_HIP(hipMemcpy(s.logits.data(), logits_.get(), s.logits.size() * 4, hipMemcpyDeviceToHost));
+    APP_HIP(hipMemcpy(s.probabilities.data(), probabilities_.get(), s.probabilities.size() * 4, hipMemcpyDeviceToHost));
+    for (const DeviceTensor &x : step_inputs_) s.activations.push_back(download(x));
+    if (alpha_) {
+      s.alpha.resize(static_cast<size_t>(d_.steps));
+      APP_HIP(hipMemcpy(s.alpha.data(), alpha_.get(), s.alpha.size() * 4, hipMemcpyDeviceToHost));
     }
-    return implementation_check();
+    return s;
   }
+
+  bool outputs_match() override;
 
   uint64_t outputs_digest() const override {
     appproto::Digest h;
-    h.add(host_generated_.get(), d_.token_count() * sizeof(int))
-        .add(host_normalized_.data(), host_normalized_.size() * 4)
-        .add(host_logits_.data(), host_logits_.size() * 4)
-        .add(host_probabilities_.data(), host_probabilities_.size() * 4);
-    for (const std::vector<uint8_t> &bytes : host_activation_bytes_) h.add(bytes.data(), bytes.size());
+    h.add(last_.generated.data(), last_.generated.size() * sizeof(int))
+        .add(last_.normalized.data(), last_.normalized.size() * 4)
+        .add(last_.logits.data(), last_.logits.size() * 4)
+        .add(last_.probabilities.data(), last_.probabilities.size() * 4)
+        .add(last_.alpha.data(), last_.alpha.size() * 4);
+    for (const PlaneBytes &planes : last_.activations)
+      for (const std::vector<uint8_t> &p : planes) h.add(p.data(), p.size());
     return h.value();
   }
 
-  // Self-test: the device conversion of a [rows][width] matrix against the host
-  // reference (NVFP4 also alpha = d * 0.75).
-  bool selftest(const std::vector<float> &m, long long rows) {
-    if (c_ == kFp32) return true;
-    DeviceArray<float> dm = device_array<float>(m.size());
-    APP_HIP(hipMemcpy(dm.get(), m.data(), m.size() * 4, hipMemcpyHostToDevice));
-    Operand o = make_operand(rows);
-    DeviceArray<float> other = device_array<float>(1), alpha = device_array<float>(1);
-    const float three_quarters = 0.75f;
-    APP_HIP(hipMemcpy(other.get(), &three_quarters, 4, hipMemcpyHostToDevice));
-    other_decode_override_ = other.get();
-    convert(dm.get(), o, alpha.get(), nullptr);
-    other_decode_override_ = nullptr;
-    APP_HIP(hipDeviceSynchronize());
-    const Quantized expected = quantize(c_, m.data(), rows, d_.width);
-    bool pass = compare("self-test", expected, download(o), rows);
-    if (c_ == kNvfp4) {
-      float got = 0.0f;
-      APP_HIP(hipMemcpy(&got, alpha.get(), 4, hipMemcpyDeviceToHost));
-      const float want = expected.decode * three_quarters;
-      if (got != want) {
-        std::fprintf(stderr, "%s: self-test alpha %.9g, expected %.9g\n", appproto::program(),
-                     static_cast<double>(got), static_cast<double>(want));
-        pass = false;
-      }
-    }
-    return pass;
-  }
+  const Format &format() const { return *format_; }
+  const WeightReading &weight_reading() const { return weights_read_; }
+  const l2c_decoder::Expectation *production() const { return production_.get(); }
+  int fault() const { return fault_; }
 
  private:
-  // Test hook (--set fault=N, check only), the reference's mutant classes
-  // planted in the downloaded step-0 activations instead of the kernels:
-  // 1 an element code one step toward zero (rounding), 2 two neighbouring
-  // block scales exchanged (scale layout); 3 (after the download) the logits
-  // divided by alpha, as a contraction that ignored alpha would leave them.
-  void plant(Quantized &q) const {
-    if (fault_ == 1) {
-      for (uint16_t &code : q.codes) {
-        const unsigned mag = c_ == kBf16 ? code & 0x7fffu : c_ == kMxfp6 ? code & 31u : code & 7u;
-        if (mag > 1) {
-          --code;
-          return;
-        }
-      }
-    } else if (fault_ == 2) {
-      for (size_t i = 0; i + 1 < q.scales.size(); i += 2)
-        if (q.scales[i] != q.scales[i + 1]) {
-          std::swap(q.scales[i], q.scales[i + 1]);
-          return;
-        }
-    }
-  }
-
-  Operand make_operand(long long rows) {
-    Operand o;
-    o.rows = rows;
-    o.width = d_.width;
-    const size_t n = static_cast<size_t>(rows * d_.width);
-    if (c_ == kBf16 || c_ == kNvfp4) {
-      o.wide_count = n;
-      o.wide = device_array<uint16_t>(n);
-    }
-    if (c_ == kMxfp6) {
-      APP_L2C(l2c_mxfp6_bytes(static_cast<int>(rows), static_cast<int>(d_.width), &o.code_bytes, &o.scale_bytes));
-    } else if (c_ == kNvfp4) {
-      o.code_bytes = n / 2;
-      o.scale_bytes = n / 16;
-      o.tensor = device_array<float>(2);
-    }
-    if (o.code_bytes) o.codes = device_array<uint8_t>(o.code_bytes);
-    if (o.scale_bytes) o.scales = device_array<uint8_t>(o.scale_bytes);
-    return o;
-  }
-
-  // FP32 [rows][width] at x -> operand o. NVFP4 activations (alpha given) get
-  // alpha = d_activations * d_weights.
-  void convert(const float *x, Operand &o, float *alpha, hipStream_t stream) {
-    const int rows = static_cast<int>(o.rows), W = static_cast<int>(d_.width);
-    const long long n = o.rows * d_.width;
-    switch (c_) {
-      case kBf16: APP_L2C(l2c_to_bf16_x4(o.wide.get(), x, n, stream)); break;
-      case kMxfp6: APP_L2C(l2c_quantize_mxfp6(o.codes.get(), o.scales.get(), x, rows, W, stream)); break;
-      case kNvfp4: {
-        const float *other = alpha ? (other_decode_override_ ? other_decode_override_ : weights_.tensor.get() + 1)
-                                   : nullptr;
-        APP_L2C(l2c_nvfp4_tensor_scales(o.tensor.get(), alpha, other, x, n, partials_.get(), stream));
-        APP_L2C(l2c_quantize_nvfp4(o.codes.get(), o.scales.get(), o.wide.get(), x, o.tensor.get(), rows, W, stream));
-        break;
-      }
-      default: break;
-    }
-  }
-
-  std::vector<float> host_weights() const {
-    if (fixture_ != 0) return host_classifier_;
-    std::vector<float> w(static_cast<size_t>(d_.vocab * d_.width), 0.0f);
-    for (long long r = 0; r < d_.vocab; ++r) w[static_cast<size_t>(r * d_.width + (r + d_.vocab - 1) % d_.vocab)] = 1.0f;
-    return w;
-  }
-
-  // Downloads and unpacks an operand.
-  Quantized download(const Operand &o) const {
-    Quantized q;
-    const size_t n = static_cast<size_t>(o.rows * d_.width);
-    q.codes.resize(n);
-    if (c_ == kBf16) {
-      APP_HIP(hipMemcpy(q.codes.data(), o.wide.get(), n * 2, hipMemcpyDeviceToHost));
-      return q;
-    }
-    std::vector<uint8_t> bytes(o.code_bytes), scale_bytes(o.scale_bytes);
-    APP_HIP(hipMemcpy(bytes.data(), o.codes.get(), o.code_bytes, hipMemcpyDeviceToHost));
-    APP_HIP(hipMemcpy(scale_bytes.data(), o.scales.get(), o.scale_bytes, hipMemcpyDeviceToHost));
-    const long long W = d_.width;
-    q.scales.resize(static_cast<size_t>(o.rows * (W / (c_ == kMxfp6 ? 32 : 16))));
-    if (c_ == kMxfp6) {
-      // Tiled operand layout: codes [W/128][Rp/32][4][32][24 B], scales [W/128][Rp][4].
-      const long long Rp = (o.rows + 31) / 32 * 32;
-      l2c_host::parallel_ranges(static_cast<size_t>(o.rows), threads(), [&](size_t r0, size_t r1, size_t) {
-        for (long long r = static_cast<long long>(r0); r < static_cast<long long>(r1); ++r)
-          for (long long kb = 0; kb < W / 32; ++kb) {
-            const long long t = kb / 4, b = kb % 4;
-            const uint8_t *block = bytes.data() + (((t * (Rp / 32) + r / 32) * 4 + b) * 32 + r % 32) * 24;
-            for (long long j = 0; j < 32; ++j)
-              q.codes[static_cast<size_t>(r * W + kb * 32 + j)] = static_cast<uint16_t>(unpack_e3m2(block, j));
-            q.scales[static_cast<size_t>(r * (W / 32) + kb)] = scale_bytes[static_cast<size_t>((t * Rp + r) * 4 + b)];
-          }
-      });
-    } else {
-      q.scales = scale_bytes;
-      l2c_host::parallel_ranges(static_cast<size_t>(o.rows), threads(), [&](size_t r0, size_t r1, size_t) {
-        for (long long r = static_cast<long long>(r0); r < static_cast<long long>(r1); ++r)
-          for (long long k = 0; k < W; ++k)
-            q.codes[static_cast<size_t>(r * W + k)] = static_cast<uint16_t>(unpack_e2m1(bytes.data() + r * (W / 2), k));
-      });
-    }
-    if (c_ == kNvfp4) {
-      float ts[2];
-      APP_HIP(hipMemcpy(ts, o.tensor.get(), 8, hipMemcpyDeviceToHost));
-      q.decode = ts[1];
-      // The bf16 expansion the contraction multiplies must be the exact value
-      // of every code and scale.
-      std::vector<uint16_t> wide(n);
-      APP_HIP(hipMemcpy(wide.data(), o.wide.get(), n * 2, hipMemcpyDeviceToHost));
-      long long bad = 0;
-      for (size_t i = 0; i < n; ++i) {
-        const long long r = static_cast<long long>(i) / d_.width, k = static_cast<long long>(i) % d_.width;
-        if (bf16_value(wide[i]) != static_cast<double>(dequantized(c_, q, d_.width, r, k))) ++bad;
-      }
-      if (bad) {
-        std::fprintf(stderr, "%s: %lld bf16 expansion values differ from their codes\n", appproto::program(), bad);
-        q.decode = NAN;  // fails the comparison
-      }
-    }
-    return q;
-  }
-
-  bool compare(const char *what, const Quantized &expected, const Quantized &actual, long long rows) const {
-    long long code_errors = 0, scale_errors = 0;
-    const char *app = appproto::program();
-    for (size_t i = 0; i < expected.codes.size(); ++i)
-      if (expected.codes[i] != actual.codes[i] && code_errors++ < kReportLimit)
-        std::fprintf(stderr, "%s: %s code mismatch row %lld column %lld: expected 0x%x, actual 0x%x\n", app, what,
-                     static_cast<long long>(i) / d_.width, static_cast<long long>(i) % d_.width, expected.codes[i],
-                     actual.codes[i]);
-    for (size_t i = 0; i < expected.scales.size(); ++i)
-      if (expected.scales[i] != actual.scales[i] && scale_errors++ < kReportLimit)
-        std::fprintf(stderr, "%s: %s scale mismatch block %zu: expected 0x%x, actual 0x%x\n", app, what, i,
-                     expected.scales[i], actual.scales[i]);
-    const bool decode_ok = expected.decode == actual.decode;
-    if (!decode_ok)
-      std::fprintf(stderr, "%s: %s tensor decode scale %.9g, expected %.9g\n", app, what,
-                   static_cast<double>(actual.decode), static_cast<double>(expected.decode));
-    std::fprintf(stderr, "%s: %s (%lld rows): %lld code and %lld scale mismatches\n", app, what, rows, code_errors,
-                 scale_errors);
-    return code_errors == 0 && scale_errors == 0 && decode_ok;
-  }
-
-  void download_diagnostics() {
-    host_normalized_.resize(d_.activation_count());
-    host_logits_.resize(d_.row_count());
-    host_probabilities_.resize(d_.row_count());
-    APP_HIP(hipMemcpy(host_normalized_.data(), normalized_.get(), host_normalized_.size() * 4, hipMemcpyDeviceToHost));
-    APP_HIP(hipMemcpy(host_logits_.data(), logits_.get(), host_logits_.size() * 4, hipMemcpyDeviceToHost));
-    APP_HIP(hipMemcpy(host_probabilities_.data(), probabilities_.get(), host_probabilities_.size() * 4,
-                     hipMemcpyDeviceToHost));
-    host_activation_bytes_.clear();
-    for (const Operand &a : activations_) {
-      std::vector<uint8_t> bytes(a.code_bytes + a.scale_bytes + a.wide_count * 2 + (a.tensor ? 8 : 0));
-      uint8_t *p = bytes.data();
-      if (a.code_bytes) APP_HIP(hipMemcpy(p, a.codes.get(), a.code_bytes, hipMemcpyDeviceToHost));
-      p += a.code_bytes;
-      if (a.scale_bytes) APP_HIP(hipMemcpy(p, a.scales.get(), a.scale_bytes, hipMemcpyDeviceToHost));
-      p += a.scale_bytes;
-      if (a.wide_count) APP_HIP(hipMemcpy(p, a.wide.get(), a.wide_count * 2, hipMemcpyDeviceToHost));
-      p += a.wide_count * 2;
-      if (a.tensor) APP_HIP(hipMemcpy(p, a.tensor.get(), 8, hipMemcpyDeviceToHost));
-      host_activation_bytes_.push_back(std::move(bytes));
-    }
-  }
-
-  const float *embedding_row(long long token, std::vector<float> &scratch) const {
-    if (fixture_ != 0) return &host_embedding_[static_cast<size_t>(token * d_.width)];
-    scratch.assign(static_cast<size_t>(d_.width), 1.0f);
-    scratch[static_cast<size_t>(token)] = 4.0f;
-    return scratch.data();
-  }
-
-  // spec.json "implementation_check": every stage against an independent host
-  // computation from the GPU's own inputs to that stage.
-  bool implementation_check() {
-    const char *app = appproto::program();
-    const long long B = d_.batch, W = d_.width, V = d_.vocab, S = d_.steps;
-    // 1. Normalized rows against rmsnorm in double of the token the GPU fed back.
-    std::atomic<int> reported{0};
-    auto report = [&]() { return reported.fetch_add(1) < kReportLimit; };
-    std::vector<long long> norm_errors(static_cast<size_t>(S * B), 0), range_errors(static_cast<size_t>(S * B), 0);
-    l2c_host::parallel_ranges(static_cast<size_t>(S * B), threads(), [&](size_t j0, size_t j1, size_t) {
-      std::vector<double> row(static_cast<size_t>(W));
-      std::vector<float> scratch;
-      for (size_t job = j0; job < j1; ++job) {
-        const long long s = static_cast<long long>(job) / B, b = static_cast<long long>(job) % B;
-        const long long token = s == 0 ? host_prompts_.get()[b] : host_generated_.get()[b * S + s - 1];
-        if (token < 0 || token >= V) {
-          range_errors[job] = 1;
-          continue;
-        }
-        rmsnorm_double(embedding_row(token, scratch), W, row.data());
-        const float *o = &host_normalized_[d_.activation_at(b, s)];
-        for (long long k = 0; k < W; ++k) {
-          const double e = row[static_cast<size_t>(k)];
-          if (!(std::fabs(o[k] - e) <= 2e-6 * std::fabs(e) + 1e-12)) {
-            if (norm_errors[job]++ == 0 && report())
-              std::fprintf(stderr, "%s: normalized mismatch step %lld sequence %lld column %lld: expected %.9g, "
-                           "actual %.9g\n", app, s, b, k, e, static_cast<double>(o[k]));
-          }
-        }
-      }
+  // The converted weights against the host quantizer of the FP32 weights,
+  // once (they are not touched by invocations), and their host values for the
+  // logit check.
+  void read_weights() {
+    const std::vector<float> w = model_.classifier();
+    weights_read_.host = quantize(case_, w.data(), d_.vocab, d_.width);
+    std::string defect;
+    const Quantized device = format_->unpack(download(weights_), d_.vocab, d_.width, &defect);
+    Stage stage("converted weights");
+    match_codes(stage, "weights", weights_read_.host, device, d_.width);
+    if (!defect.empty()) stage.failed("weights: %s", defect.c_str());
+    weights_read_.values = static_cast<long long>(w.size());
+    weights_read_.differing = stage.failures();
+    weights_read_.values_f.resize(w.size());
+    spread(d_.vocab, [&](long long r) {
+      for (long long k = 0; k < d_.width; ++k)
+        weights_read_.values_f[static_cast<size_t>(r * d_.width + k)] = dequantized(case_, weights_read_.host, d_.width, r, k);
     });
-    long long normalized_errors = 0, token_range_errors = 0;
-    for (size_t i = 0; i < norm_errors.size(); ++i) normalized_errors += norm_errors[i], token_range_errors += range_errors[i];
+  }
 
-    // 2. Converted activations, bit for bit, every step (and NVFP4 alpha).
-    bool activations_ok = true;
-    std::vector<std::vector<float>> act(static_cast<size_t>(S));
-    std::vector<float> alpha(static_cast<size_t>(S), 1.0f);
-    if (c_ != kFp32) {
-      for (long long s = 0; s < S; ++s) {
-        const Quantized expected = quantize(c_, &host_normalized_[d_.activation_at(0, s)], B, W);
-        char what[48];
-        std::snprintf(what, sizeof what, "activations step %lld", s);
-        Quantized actual = download(activations_[static_cast<size_t>(s)]);
-        if (s == 0) plant(actual);
-        activations_ok = compare(what, expected, actual, B) && activations_ok;
-        std::vector<float> &a = act[static_cast<size_t>(s)];
-        a.resize(static_cast<size_t>(B * W));
-        for (long long b = 0; b < B; ++b)
-          for (long long k = 0; k < W; ++k) a[static_cast<size_t>(b * W + k)] = dequantized(c_, expected, W, b, k);
-        if (c_ == kNvfp4) {
-          alpha[static_cast<size_t>(s)] = expected.decode * weight_decode_;
-          if (s == 0) alpha_host_ = alpha[0];
-          float got = 0.0f;
-          APP_HIP(hipMemcpy(&got, alpha_.get() + s, 4, hipMemcpyDeviceToHost));
-          if (got != alpha[static_cast<size_t>(s)]) {
-            std::fprintf(stderr, "%s: alpha step %lld %.9g, expected %.9g\n", app, s, static_cast<double>(got),
-                         static_cast<double>(alpha[static_cast<size_t>(s)]));
-            activations_ok = false;
-          }
-        }
-      }
+  int case_;
+  Dims d_;
+  HostModel model_;
+  int fault_;
+  std::unique_ptr<Format> format_;
+  DeviceArray<float> embedding_, classifier_, norm_weight_, normalized_, logits_, probabilities_, alpha_;
+  DeviceArray<int> prompts_, tokens_, generated_;
+  PinnedArray<int> pinned_prompts_, pinned_generated_;
+  DeviceTensor weights_;
+  std::vector<DeviceTensor> step_inputs_;
+  double setup_encode_ms_ = 0.0;
+  WeightReading weights_read_;
+  std::unique_ptr<l2c_decoder::Expectation> production_;
+  Snapshot last_;
+};
+
+// ---------------------------------------------------------------------------
+// Audit: spec.json "implementation_check". Each stage compares one thing the
+// GPU produced with a host computation from the GPU's own inputs to that
+// stage, so an implementation passes whatever its precision.
+
+class Audit {
+ public:
+  Audit(const ClassifierExperiment &app, const Snapshot &got) : app_(app), got_(got), d_(app.dims()) {}
+
+  bool run() {
+    Stage normalized("normalized rows"), weights("converted weights"), inputs("converted activations"),
+        logits("logits"), probabilities("probabilities"), tokens("tokens");
+    check_normalized(normalized);
+    const WeightReading &w = app_.weight_reading();
+    weights.compared(w.values);
+    if (w.differing) weights.failed_silently(w.differing);  // printed when the weights were read
+    const std::vector<std::vector<float>> inputs_f = check_inputs(inputs);
+    check_logits(logits, inputs_f);
+    check_distribution(probabilities, tokens);
+    const Stage *stages[] = {&normalized, &weights, &inputs, &logits, &probabilities, &tokens};
+    bool pass = true;
+    std::string summary;
+    for (const Stage *s : stages) {
+      pass = pass && s->ok();
+      summary += (summary.empty() ? "" : "; ") + s->tally();
     }
-
-    // 3. Logits of up to 8 sequences, every step and row, against the double
-    // product of the operands the GPU multiplied; the bound holds for FP32
-    // accumulation in any order.
-    std::vector<long long> sampled;
-    const long long count = std::min<long long>(8, B);
-    for (long long i = 0; i < count; ++i) sampled.push_back(count == 1 ? 0 : i * (B - 1) / (count - 1));
-    const double u = 0x1p-23, gamma = static_cast<double>(W) * u / (1.0 - static_cast<double>(W) * u);
-    const std::vector<float> fp32_weights = c_ == kFp32 ? host_weights() : std::vector<float>();
-    const std::vector<float> &weights = c_ == kFp32 ? fp32_weights : dequantized_weights_;
-    std::vector<long long> logit_errors(static_cast<size_t>(count * S), 0);
-    std::vector<double> worst(static_cast<size_t>(count * S), 0.0);
-    l2c_host::parallel_ranges(static_cast<size_t>(count * S), threads(), [&](size_t j0, size_t j1, size_t) {
-      for (size_t job = j0; job < j1; ++job) {
-        const long long i = static_cast<long long>(job) / S, s = static_cast<long long>(job) % S;
-        const long long b = sampled[static_cast<size_t>(i)];
-        const float *a = c_ == kFp32 ? &host_normalized_[d_.activation_at(b, s)] : &act[static_cast<size_t>(s)][static_cast<size_t>(b * W)];
-        const double scale = alpha[static_cast<size_t>(s)];
-        for (long long r = 0; r < V; ++r) {
-          const float *w = &weights[static_cast<size_t>(r * W)];
-          double sum = 0.0, mag = 0.0;
-          for (long long k = 0; k < W; ++k) {
-            const double p = static_cast<double>(a[k]) * static_cast<double>(w[k]);
-            sum += p;
-            mag += std::fabs(p);
-          }
-          const double expected = sum * scale;
-          const double actual = host_logits_[d_.row_at(b, s) + static_cast<size_t>(r)];
-          const double bound = gamma * mag * std::fabs(scale) + u * std::fabs(expected) + 1e-30;
-          const double error = std::fabs(actual - expected);
-          if (!(error <= bound)) {
-            if (logit_errors[job]++ == 0)
-              std::fprintf(stderr, "%s: logit mismatch step %lld sequence %lld row %lld: expected %.9g, actual %.9g, "
-                           "bound %.3g\n", app, s, b, r, expected, actual, bound);
-          } else if (mag > 0) {
-            worst[job] = std::max(worst[job], error / (mag * std::fabs(scale)));
-          }
-        }
-      }
-    });
-    long long total_logit_errors = 0;
-    double worst_logit = 0.0;
-    for (size_t j = 0; j < logit_errors.size(); ++j) total_logit_errors += logit_errors[j], worst_logit = std::max(worst_logit, worst[j]);
-
-    // 4. Probabilities and tokens from the GPU's own logits.
-    std::vector<long long> prob_errors(static_cast<size_t>(S * B), 0), tok_errors(static_cast<size_t>(S * B), 0);
-    l2c_host::parallel_ranges(static_cast<size_t>(S * B), threads(), [&](size_t j0, size_t j1, size_t) {
-      std::vector<double> l(static_cast<size_t>(V)), p(static_cast<size_t>(V));
-      for (size_t job = j0; job < j1; ++job) {
-        const long long s = static_cast<long long>(job) / B, b = static_cast<long long>(job) % B;
-        const float *gl = &host_logits_[d_.row_at(b, s)];
-        const float *gp = &host_probabilities_[d_.row_at(b, s)];
-        for (long long r = 0; r < V; ++r) l[static_cast<size_t>(r)] = gl[r];
-        softmax_double(l.data(), V, p.data());
-        long long best = 0;
-        for (long long r = 0; r < V; ++r) {
-          const double e = p[static_cast<size_t>(r)];
-          if (!(std::fabs(gp[r] - e) <= 2e-5 * std::fabs(e) + 1e-12) && prob_errors[job]++ == 0 && report())
-            std::fprintf(stderr, "%s: probability mismatch step %lld sequence %lld row %lld: expected %.9g, actual "
-                         "%.9g\n", app, s, b, r, e, static_cast<double>(gp[r]));
-          if (gp[r] > gp[best]) best = r;
-        }
-        if (host_generated_.get()[b * S + s] != best) {
-          tok_errors[job] = 1;
-          if (report())
-            std::fprintf(stderr, "%s: token step %lld sequence %lld is %d, the first largest probability is at "
-                         "%lld\n", app, s, b, host_generated_.get()[b * S + s], best);
-        }
-      }
-    });
-    long long probability_errors = 0, token_errors = 0;
-    for (size_t j = 0; j < prob_errors.size(); ++j) probability_errors += prob_errors[j], token_errors += tok_errors[j];
-
-    bool pass = normalized_errors == 0 && token_range_errors == 0 && activations_ok && weights_match_ &&
-                total_logit_errors == 0 && probability_errors == 0 && token_errors == 0;
-    std::fprintf(stderr,
-                 "%s: implementation check %s: normalized %lld mismatches, %lld tokens out of range; converted "
-                 "weights %s, activations %s; logits %lld mismatches over %lld sequences x %lld steps (worst "
-                 "|error| / sum|terms| %.3g, bound %.3g); probabilities %lld mismatches; tokens %lld not the first "
-                 "largest probability\n",
-                 app, pass ? "PASS" : "FAIL", normalized_errors, token_range_errors, weights_match_ ? "exact" : "MISMATCH",
-                 activations_ok ? "exact" : "MISMATCH", total_logit_errors, count, S, worst_logit, gamma,
-                 probability_errors, token_errors);
-    if (contract_) {
-      // The control must also pass the production contract check unchanged.
-      const bool production = l2c_decoder::verify(d_, *contract_, {host_generated_.get(), host_normalized_.data(),
-                                                                   host_logits_.data(), host_probabilities_.data()});
+    std::fprintf(stderr, "%s: implementation check %s: %s\n", appproto::program(), pass ? "PASS" : "FAIL",
+                 summary.c_str());
+    if (const l2c_decoder::Expectation *want = app_.production()) {
+      // The FP32 control also passes the decoder's own contract check.
+      const bool production = l2c_decoder::verify(
+          d_, *want, {got_.generated.data(), got_.normalized.data(), got_.logits.data(), got_.probabilities.data()});
       pass = pass && production;
     }
     return pass;
   }
 
-  int c_;
-  l2c_decoder::Dims d_;
-  int fixture_;
-  int fault_;
-  float alpha_host_ = 1.0f;
-  DeviceArray<float> embedding_, classifier_, norm_weight_, normalized_, logits_, probabilities_, partials_, alpha_;
-  DeviceArray<int> prompts_, tokens_, generated_;
-  PinnedArray<int> host_prompts_, host_generated_;
-  std::vector<float> host_embedding_, host_classifier_;
-  Operand weights_;
-  std::vector<Operand> activations_;
-  const float *other_decode_override_ = nullptr;
-  std::vector<float> dequantized_weights_;
-  float weight_decode_ = 1.0f;
-  bool weights_match_ = true;
-  std::unique_ptr<l2c_decoder::Expectation> contract_;
-  std::vector<float> host_normalized_, host_logits_, host_probabilities_;
-  std::vector<std::vector<uint8_t>> host_activation_bytes_;
+ private:
+  int token_fed(long long b, long long s) const {
+    return s == 0 ? static_cast<int>(app_.model().prompt(b)) : got_.generated[static_cast<size_t>(b * d_.steps + s - 1)];
+  }
+
+  // Every (step, sequence) row against rmsnorm in double of the embedding row
+  // of the token the GPU fed into that step.
+  void check_normalized(Stage &stage) {
+    stage.compared(d_.steps * d_.batch);
+    spread(d_.steps * d_.batch, [&](long long job) {
+      const long long s = job / d_.batch, b = job % d_.batch;
+      const int token = token_fed(b, s);
+      if (token < 0 || token >= d_.vocab) {
+        stage.failed("step %lld sequence %lld was fed token %d, outside the vocabulary", s, b, token);
+        return;
+      }
+      std::vector<double> want(static_cast<size_t>(d_.width));
+      std::vector<float> scratch;
+      rmsnorm_double(app_.model().embedding_row(token, &scratch), d_.width, want.data());
+      const float *row = &got_.normalized[d_.activation_at(b, s)];
+      for (long long k = 0; k < d_.width; ++k) {
+        const double e = want[static_cast<size_t>(k)];
+        if (!(std::fabs(row[k] - e) <= l2c_decoder::kActivationTolerance * std::fabs(e) + l2c_decoder::kToleranceFloor)) {
+          stage.failed("normalized mismatch at step %lld sequence %lld column %lld: host %.9g, device %.9g", s, b, k, e,
+                       static_cast<double>(row[k]));
+          return;  // one report per row
+        }
+      }
+    });
+  }
+
+  // Each step's converted activations, bit for bit, against the host
+  // quantizer of that step's GPU-normalized rows, and NVFP4's alpha against
+  // d(activations) * d(weights). Returns the host values of the activations
+  // (without the NVFP4 tensor scale), the operands the logit check multiplies.
+  std::vector<std::vector<float>> check_inputs(Stage &stage) {
+    const int c = app_.lowprec_case();
+    std::vector<std::vector<float>> values(static_cast<size_t>(d_.steps));
+    if (c == kFp32) return values;
+    for (long long s = 0; s < d_.steps; ++s) {
+      const Quantized host = quantize(c, &got_.normalized[d_.activation_at(0, s)], d_.batch, d_.width);
+      std::string defect;
+      Quantized device = app_.format().unpack(got_.activations[static_cast<size_t>(s)], d_.batch, d_.width, &defect);
+      if (s == 0) plant(device);
+      char what[40];
+      std::snprintf(what, sizeof what, "step %lld", s);
+      match_codes(stage, what, host, device, d_.width);
+      if (!defect.empty()) stage.failed("%s: %s", what, defect.c_str());
+      if (c == kNvfp4) {
+        const float want = host.decode * app_.weight_reading().host.decode;
+        const float have = got_.alpha[static_cast<size_t>(s)];
+        stage.compared(1);
+        if (!(have == want)) stage.failed("%s alpha mismatch: host %.9g, device %.9g", what, static_cast<double>(want), static_cast<double>(have));
+      }
+      std::vector<float> &v = values[static_cast<size_t>(s)];
+      v.resize(static_cast<size_t>(d_.batch * d_.width));
+      spread(d_.batch, [&](long long b) {
+        for (long long k = 0; k < d_.width; ++k) v[static_cast<size_t>(b * d_.width + k)] = dequantized(c, host, d_.width, b, k);
+      });
+    }
+    return values;
+  }
+
+  void plant(Quantized &q) const {
+    const int c = app_.lowprec_case();
+    if (app_.fault() == ClassifierExperiment::kRounding) {
+      const unsigned magnitude_mask = c == kBf16 ? 0x7fffu : c == kMxfp6 ? 0x1fu : 0x7u;
+      auto it = std::find_if(q.codes.begin(), q.codes.end(), [&](uint16_t v) { return (v & magnitude_mask) > 1; });
+      if (it != q.codes.end()) --*it;
+    } else if (app_.fault() == ClassifierExperiment::kScaleLayout) {
+      for (size_t i = 0; i + 1 < q.scales.size(); i += 2)
+        if (q.scales[i] != q.scales[i + 1]) {
+          std::swap(q.scales[i], q.scales[i + 1]);
+          break;
+        }
+    }
+  }
+
+  // Logits of up to 8 sequences spread over the batch (first and last
+  // included), every step and vocabulary row, against the double product of
+  // the host values of both operands times alpha. The bound gamma_K *
+  // sum|a_k w_k| * |alpha| + 2^-23 |expected| + 1e-30, gamma_K = K u / (1 - K u)
+  // with u = 2^-23, holds for FP32 accumulation in any order.
+  void check_logits(Stage &stage, const std::vector<std::vector<float>> &inputs_f) {
+    const int c = app_.lowprec_case();
+    const long long probes = std::min<long long>(8, d_.batch);
+    const double u = 0x1p-23, K = static_cast<double>(d_.width), gamma = K * u / (1.0 - K * u);
+    std::vector<float> fp32_weights;
+    if (c == kFp32) fp32_weights = app_.model().classifier();
+    const std::vector<float> &weights = c == kFp32 ? fp32_weights : app_.weight_reading().values_f;
+    stage.compared(probes * d_.steps * d_.vocab);
+    spread(probes * d_.steps, [&](long long job) {
+      const long long i = job / d_.steps, s = job % d_.steps;
+      const long long b = probes == 1 ? 0 : i * (d_.batch - 1) / (probes - 1);
+      const float *a = c == kFp32 ? &got_.normalized[d_.activation_at(b, s)]
+                                  : &inputs_f[static_cast<size_t>(s)][static_cast<size_t>(b * d_.width)];
+      const double alpha = c == kNvfp4 ? static_cast<double>(got_.alpha[static_cast<size_t>(s)]) : 1.0;
+      const float *have = &got_.logits[d_.row_at(b, s)];
+      double worst = 0.0;
+      for (long long r = 0; r < d_.vocab; ++r) {
+        const float *w = &weights[static_cast<size_t>(r * d_.width)];
+        double dot = 0.0, magnitude = 0.0;
+        for (long long k = 0; k < d_.width; ++k) {
+          const double term = static_cast<double>(a[k]) * w[k];
+          dot += term;
+          magnitude += std::fabs(term);
+        }
+        const double want = dot * alpha;
+        const double bound = gamma * magnitude * std::fabs(alpha) + u * std::fabs(want) + 1e-30;
+        const double error = std::fabs(static_cast<double>(have[r]) - want);
+        if (error <= bound) {
+          worst = std::max(worst, error / bound);
+        } else {
+          stage.failed("logit mismatch at step %lld sequence %lld row %lld: host %.9g, device %.9g, bound %.3g", s, b, r,
+                       want, static_cast<double>(have[r]), bound);
+        }
+      }
+      stage.worst(worst);
+    });
+  }
+
+  // Every (step, sequence): the probabilities against softmax in double of
+  // the GPU's own logits, and the token against the first largest
+  // probability the GPU wrote.
+  void check_distribution(Stage &probabilities, Stage &tokens) {
+    probabilities.compared(d_.steps * d_.batch);
+    tokens.compared(d_.steps * d_.batch);
+    spread(d_.steps * d_.batch, [&](long long job) {
+      const long long s = job / d_.batch, b = job % d_.batch;
+      const float *logits = &got_.logits[d_.row_at(b, s)];
+      const float *p = &got_.probabilities[d_.row_at(b, s)];
+      std::vector<double> wide(logits, logits + d_.vocab), want(static_cast<size_t>(d_.vocab));
+      softmax_double(wide.data(), d_.vocab, want.data());
+      for (long long r = 0; r < d_.vocab; ++r) {
+        const double e = want[static_cast<size_t>(r)];
+        if (!(std::fabs(p[r] - e) <= l2c_decoder::kProbabilityTolerance * std::fabs(e) + l2c_decoder::kToleranceFloor)) {
+          probabilities.failed("probability mismatch at step %lld sequence %lld row %lld: host %.9g, device %.9g", s, b,
+                               r, e, static_cast<double>(p[r]));
+          break;
+        }
+      }
+      const long long first_largest = std::max_element(p, p + d_.vocab) - p;
+      const int token = got_.generated[static_cast<size_t>(b * d_.steps + s)];
+      if (token != first_largest)
+        tokens.failed("token mismatch at step %lld sequence %lld: device %d, first largest probability at %lld", s, b,
+                      token, first_largest);
+    });
+  }
+
+  const ClassifierExperiment &app_;
+  const Snapshot &got_;
+  const Dims d_;
 };
 
-// Dimensions with the decoder contract's limits and the experiment's alignment
-// (decoder_lowprec.cu:1106-1127; scripts match the messages).
-std::unique_ptr<LowprecWorkload> make_lowprec(int c, long long batch, long long width, long long vocab, long long steps,
-                                              long long fixture, long long fault = 0) {
-  using appproto::abort_run;
-  using appproto::kUsage;
-  if (fixture < 0 || fixture > 3) abort_run(kUsage, "fixture must be 0 (primary model) or 1, 2, 3 (got %lld)", fixture);
-  if (batch < 1 || batch > (1LL << 20)) abort_run(kUsage, "batch must be in [1, 1048576] (got %lld)", batch);
-  if (width < 2 || width > (1LL << 24) - 16) abort_run(kUsage, "width must be in [2, 16777200] (got %lld)", width);
-  if (vocab < 2 || vocab > width)
-    abort_run(kUsage, "vocab must satisfy 2 <= vocab <= width (got %lld, %lld)", vocab, width);
-  if (steps < 2 || steps > 1024) abort_run(kUsage, "steps must be in [2, 1024] (got %lld)", steps);
-  const long long max_fault = c == kNvfp4 ? 3 : c == kMxfp6 ? 2 : c == kBf16 ? 1 : 0;
-  if (fault < 0 || fault > max_fault)
-    abort_run(kUsage, "fault must be in [0, %lld] for case %s (got %lld)", max_fault, case_name(c), fault);
-  if (c != kFp32 && (width % 128 != 0 || vocab % 4 != 0))
-    abort_run(kUsage, "low precision cases need width %% 128 == 0 and vocab %% 4 == 0 (got width %lld, vocab %lld)",
-         width, vocab);
+bool ClassifierExperiment::outputs_match() {
+  last_ = snapshot();
+  if (fault_ == kAlpha)
+    for (long long s = 0; s < d_.steps; ++s)
+      for (size_t i = d_.row_at(0, s); i < d_.row_at(0, s + 1); ++i) last_.logits[i] /= last_.alpha[static_cast<size_t>(s)];
+  return Audit(*this, last_).run();
+}
+
+// ---------------------------------------------------------------------------
+// Dimensions: the decoder contract's limits, the cases' alignment, and the
+// device memory the run needs (decoder_lowprec.cu:1106-1127 for the limits;
+// tests match the wording).
+
+void require(bool holds, const char *format, ...) __attribute__((format(printf, 2, 3)));
+void require(bool holds, const char *format, ...) {
+  if (holds) return;
+  char reason[256];
+  va_list args;
+  va_start(args, format);
+  std::vsnprintf(reason, sizeof reason, format, args);
+  va_end(args);
+  throw appproto::Abort(appproto::kUsage, reason);
+}
+
+// Device bytes per value of one encoded operand.
+double encoded_bytes_per_value(int c) {
+  switch (c) {
+    case kBf16: return 2.0;
+    case kMxfp6: return 0.75 + 1.0 / 32.0;
+    case kNvfp4: return 0.5 + 1.0 / 16.0 + 2.0;
+    default: return 0.0;
+  }
+}
+
+std::unique_ptr<ClassifierExperiment> build_experiment(int c, const Dims &d, long long fixture, long long fault) {
+  require(fixture >= 0 && fixture <= 3, "fixture must be 0 (primary model) or 1, 2, 3 (got %lld)", fixture);
+  require(d.batch >= 1 && d.batch <= (1LL << 20), "batch must be in [1, 1048576] (got %lld)", d.batch);
+  require(d.width >= 2 && d.width <= (1LL << 24) - 16, "width must be in [2, 16777200] (got %lld)", d.width);
+  require(d.vocab >= 2 && d.vocab <= d.width, "vocab must satisfy 2 <= vocab <= width (got %lld, %lld)", d.vocab,
+          d.width);
+  require(d.steps >= 2 && d.steps <= 1024, "steps must be in [2, 1024] (got %lld)", d.steps);
+  const long long most = c == kNvfp4 ? 3 : c == kMxfp6 ? 2 : c == kBf16 ? 1 : 0;
+  require(fault >= 0 && fault <= most, "fault must be in [0, %lld] for case %s (got %lld)", most, case_name(c), fault);
+  require(c == kFp32 || (d.width % 128 == 0 && d.vocab % 4 == 0),
+          "low precision cases need width %% 128 == 0 and vocab %% 4 == 0 (got width %lld, vocab %lld)", d.width,
+          d.vocab);
+  const double W = static_cast<double>(d.width), V = static_cast<double>(d.vocab), B = static_cast<double>(d.batch),
+               S = static_cast<double>(d.steps);
+  const double bytes = 4.0 * 2.0 * V * W + 4.0 * S * B * (W + 2.0 * V) + encoded_bytes_per_value(c) * (V + S * B) * W;
   const double gib = static_cast<double>(1LL << 30);
-  const double device = 4.0 * (2.0 * static_cast<double>(vocab) * width) +
-                        4.0 * static_cast<double>(steps) * batch * (static_cast<double>(width) + 2.0 * vocab) +
-                        2.0 * (static_cast<double>(vocab) + steps * static_cast<double>(batch)) * width;
-  if (device > kDeviceLimitGiB * gib)
-    abort_run(kUsage, "dimensions need %.1f GiB of device memory (limit %.0f)", device / gib, kDeviceLimitGiB);
-  return std::make_unique<LowprecWorkload>(c, batch, width, vocab, steps, static_cast<int>(fixture),
-                                           static_cast<int>(fault));
+  require(bytes <= kDeviceLimitGiB * gib, "dimensions need %.1f GiB of device memory (limit %.0f)", bytes / gib,
+          kDeviceLimitGiB);
+  HostModel model = fixture == 0 ? HostModel::synthetic(d.width, d.vocab)
+                                 : HostModel::dense(static_cast<int>(fixture), d.width, d.vocab);
+  return std::make_unique<ClassifierExperiment>(c, d, std::move(model), static_cast<int>(fault));
 }
 
 int g_case = kFp32;
 
-std::unique_ptr<appproto::Application> make_workload(const std::string &preset, appproto::Settings &settings,
-                                                     appproto::Assets &) {
+std::unique_ptr<appproto::Application> protocol_factory(const std::string &preset, appproto::Settings &settings,
+                                                        appproto::Assets &) {
   const long long fixture = settings.integer("fixture", 0);
-  const bool dense = fixture != 0;
-  const long long batch = settings.integer("batch", dense ? kFixtureBatch : kLargeBatch);
-  const long long width = settings.integer("width", dense ? kFixtureWidth : kLargeWidth);
-  const long long vocab = settings.integer("vocab", dense ? kFixtureVocab : kLargeVocab);
-  const long long steps = settings.integer("steps", kLargeSteps);
+  const Dims &shape = fixture != 0 ? kFixtureShape : kPrimary;
+  const Dims d{settings.integer("batch", shape.batch), settings.integer("width", shape.width),
+               settings.integer("vocab", shape.vocab), settings.integer("steps", kPrimary.steps)};
   const long long fault = settings.integer("fault", 0);
   if (preset != "large") return nullptr;
-  return make_lowprec(g_case, batch, width, vocab, steps, fixture, fault);
+  return build_experiment(g_case, d, fixture, fault);
 }
 
 // ---------------------------------------------------------------------------
-// --selftest: crafted rows through the device conversion against the host
-// reference (element and scale ties, saturation, zero, tiny and subnormal
-// blocks; 130 rows).
+// --selftest: a crafted matrix through the device conversion against the host
+// quantizer: element and scale ties, saturation, zero, tiny and subnormal-
+// scale blocks, 130 rows so the row padding of the tiled layouts is used.
+
 std::vector<float> crafted(long long rows, long long width) {
   std::vector<float> m(static_cast<size_t>(rows * width), 0.0f);
   auto at = [&](long long r, long long k) -> float & { return m[static_cast<size_t>(r * width + k)]; };
@@ -732,179 +783,176 @@ std::vector<float> crafted(long long rows, long long width) {
 
 int run_selftest(int c) {
   const long long rows = 130, width = 256;
-  auto workload = make_lowprec(c, rows, width, 128, 2, 0);
-  hipStream_t stream;
-  APP_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
-  workload->prepare(stream);
-  const bool pass = workload->selftest(crafted(rows, width), rows);
-  (void)hipStreamDestroy(stream);
+  bool pass = true;
+  if (c != kFp32) {
+    const std::vector<float> m = crafted(rows, width);
+    std::unique_ptr<Format> format = make_format(c);
+    DeviceArray<float> x = device_array<float>(m.size()), partner = device_array<float>(1),
+                       alpha = device_array<float>(1);
+    const float partner_decode = 0.75f;  // stands in for the weights' decode scale
+    APP_HIP(hipMemcpy(x.get(), m.data(), m.size() * 4, hipMemcpyHostToDevice));
+    APP_HIP(hipMemcpy(partner.get(), &partner_decode, 4, hipMemcpyHostToDevice));
+    DeviceTensor t = format->allocate(rows, width);
+    format->encode(x.get(), t, alpha.get(), partner.get(), nullptr);
+    APP_HIP(hipDeviceSynchronize());
+    std::string defect;
+    const Quantized device = format->unpack(download(t), rows, width, &defect);
+    const Quantized host = quantize(c, m.data(), rows, width);
+    Stage stage("self-test");
+    match_codes(stage, "crafted matrix", host, device, width);
+    if (!defect.empty()) stage.failed("%s", defect.c_str());
+    if (c == kNvfp4) {
+      float have = 0.0f;
+      APP_HIP(hipMemcpy(&have, alpha.get(), 4, hipMemcpyDeviceToHost));
+      const float want = host.decode * partner_decode;
+      stage.compared(1);
+      if (!(have == want)) stage.failed("alpha %.9g, host %.9g", static_cast<double>(have), static_cast<double>(want));
+    }
+    std::fprintf(stderr, "%s: %s\n", appproto::program(), stage.tally().c_str());
+    pass = stage.ok();
+  }
   std::printf("%s: %s quantizer self-test\n", pass ? "PASS" : "FAIL", case_name(c));
   return pass ? appproto::kPass : appproto::kMismatch;
 }
 
 // ---------------------------------------------------------------------------
-// --accuracy (spec.json "accuracy"): the primary model and the three fixtures.
-appproto::Json metrics_json(const ErrorMetrics &m) {
-  using appproto::Json;
-  Json j = Json::object();
-  j.add("rows", Json::whole(m.rows))
-      .add("max_abs_error", Json::real(m.max_abs_error))
-      .add("normalized_rms_error", Json::real(m.normalized_rms_error))
-      .add("max_abs_probability_error", Json::real(m.max_abs_probability_error))
-      .add("mean_total_variation", Json::real(m.mean_total_variation))
-      .add("top1_agree", Json::whole(m.top1_agree));
-  return j;
-}
+// Assessment: one dataset of --accuracy (spec.json "accuracy").
+//   classifier error  the case's classifier alone on fixed step-0 activations
+//                     (rmsnorm of each prompt's embedding row on the host, in
+//                     float with a sequential square sum) against double
+//                     logits of those activations and the FP32 weights
+//   token agreement   one complete decode against the model's exact tokens
+//   production        the decoder's contract check of that decode (primary)
 
-appproto::Json accuracy_dataset(int c, int fixture, hipStream_t stream, double *weight_ms) {
-  using appproto::Json;
-  auto w = fixture == 0 ? make_lowprec(c, kLargeBatch, kLargeWidth, kLargeVocab, kLargeSteps, 0)
-                        : make_lowprec(c, kFixtureBatch, kFixtureWidth, kFixtureVocab, kLargeSteps, fixture);
-  LowprecWorkload &d = *w;
-  d.prepare(stream);
-  APP_HIP(hipStreamSynchronize(stream));
-  const long long B = d.batch(), W = d.width(), V = d.vocab(), S = d.steps();
-  if (weight_ms) {
-    std::vector<double> times;
-    hipEvent_t start, stop;
-    APP_HIP(hipEventCreate(&start));
-    APP_HIP(hipEventCreate(&stop));
-    for (int i = 0; i < 5; ++i) {
-      APP_HIP(hipEventRecord(start, stream));
-      d.convert_weights(stream);
-      APP_HIP(hipEventRecord(stop, stream));
-      APP_HIP(hipEventSynchronize(stop));
-      float ms = 0.0f;
-      APP_HIP(hipEventElapsedTime(&ms, start, stop));
-      times.push_back(ms);
-    }
-    (void)hipEventDestroy(start);
-    (void)hipEventDestroy(stop);
-    std::sort(times.begin(), times.end());
-    *weight_ms = times[2];
+class Assessment {
+ public:
+  Assessment(int c, int fixture) : fixture_(fixture) {
+    const Dims &shape = fixture == 0 ? kPrimary : kFixtureShape;
+    app_ = build_experiment(c, shape, fixture, 0);
   }
-  // Fixed FP32 reference activations: step-0 rows, rmsnorm in float on the host.
-  std::vector<float> row(static_cast<size_t>(W)), activations(static_cast<size_t>(B * W));
-  auto embedding = [&](long long token) -> const float * {
-    if (fixture != 0) return &d.host_embedding()[static_cast<size_t>(token * W)];
-    std::fill(row.begin(), row.end(), 1.0f);
-    row[static_cast<size_t>(token)] = 4.0f;
-    return row.data();
-  };
-  for (long long b = 0; b < B; ++b) rmsnorm_float(embedding(b % V), W, &activations[static_cast<size_t>(b * W)]);
-  APP_HIP(hipMemcpyAsync(d.normalized(0), activations.data(), activations.size() * 4, hipMemcpyHostToDevice, stream));
-  d.enqueue_classifier(0, stream);
-  APP_HIP(hipStreamSynchronize(stream));
-  std::vector<float> logits(static_cast<size_t>(B * V));
-  APP_HIP(hipMemcpy(logits.data(), d.logits(0), logits.size() * 4, hipMemcpyDeviceToHost));
-  std::vector<double> reference(static_cast<size_t>(B * V)), actual(logits.begin(), logits.end());
-  l2c_host::parallel_ranges(static_cast<size_t>(B), threads(), [&](size_t b0, size_t b1, size_t) {
-    for (long long b = static_cast<long long>(b0); b < static_cast<long long>(b1); ++b) {
-      const float *x = &activations[static_cast<size_t>(b * W)];
-      for (long long r = 0; r < V; ++r) {
-        double sum = 0.0;
-        if (fixture == 0) {
-          sum = x[(r + V - 1) % V];  // the one nonzero weight, 1.0
-        } else {
-          const float *wr = &d.host_classifier()[static_cast<size_t>(r * W)];
-          for (long long k = 0; k < W; ++k) sum += static_cast<double>(x[k]) * wr[k];
-        }
-        reference[static_cast<size_t>(b * V + r)] = sum;
-      }
-    }
-  });
-  const ErrorMetrics classifier = compare_logits(reference, actual, B, V);
 
-  // A complete decode (one application-scope invocation).
-  d.scramble_outputs(stream);
-  d.enqueue(appproto::Scope::kApplication, stream);
-  APP_HIP(hipStreamSynchronize(stream));
-  std::vector<int> expected(static_cast<size_t>(B * S));
-  if (fixture == 0) {
-    for (long long b = 0; b < B; ++b)
-      for (long long s = 0; s < S; ++s) expected[static_cast<size_t>(b * S + s)] = static_cast<int>((b % V + s + 1) % V);
-  } else {
-    l2c_host::parallel_ranges(static_cast<size_t>(B), threads(), [&](size_t b0, size_t b1, size_t) {
-      std::vector<double> o(static_cast<size_t>(W)), l(static_cast<size_t>(V));
-      for (long long b = static_cast<long long>(b0); b < static_cast<long long>(b1); ++b) {
-        long long token = b % V;
-        for (long long s = 0; s < S; ++s) {
-          rmsnorm_double(&d.host_embedding()[static_cast<size_t>(token * W)], W, o.data());
-          for (long long r = 0; r < V; ++r) {
-            const float *wr = &d.host_classifier()[static_cast<size_t>(r * W)];
-            double sum = 0.0;
-            for (long long k = 0; k < W; ++k) sum += o[static_cast<size_t>(k)] * wr[k];
-            l[static_cast<size_t>(r)] = sum;
-          }
-          token = argmax_first(l.data(), V);
-          expected[static_cast<size_t>(b * S + s)] = static_cast<int>(token);
-        }
+  Json run(hipStream_t stream, double *weight_ms) {
+    ClassifierExperiment &app = *app_;
+    app.prepare(stream);
+    APP_HIP(hipStreamSynchronize(stream));
+    if (weight_ms) *weight_ms = median_weight_encode_ms(stream, 5);
+    const ErrorMetrics error = classifier_error(stream);
+    const Dims &d = app.dims();
+    app.scramble_outputs(stream);
+    app.enqueue(appproto::Scope::kApplication, stream);
+    APP_HIP(hipStreamSynchronize(stream));
+    const Snapshot got = app.snapshot();
+    const std::vector<int> want = app.model().reference_tokens(d.batch, d.steps);
+    Json per_step = Json::list();
+    long long agree = 0;
+    for (long long s = 0; s < d.steps; ++s) {
+      long long n = 0;
+      for (long long b = 0; b < d.batch; ++b) {
+        const size_t at = static_cast<size_t>(b * d.steps + s);
+        n += got.generated[at] == want[at];
       }
+      per_step.push(Json::whole(n));
+      agree += n;
+    }
+    Json tokens = Json::object();
+    tokens.add("agree", Json::whole(agree))
+        .add("total", Json::whole(d.batch * d.steps))
+        .add("per_step_agree", std::move(per_step))
+        .add("reference", Json::text(fixture_ == 0 ? "analytic progression" : "double host decode"));
+    Json errors = Json::object();
+    errors.add("rows", Json::whole(error.rows))
+        .add("max_abs_error", Json::real(error.max_abs_error))
+        .add("normalized_rms_error", Json::real(error.normalized_rms_error))
+        .add("max_abs_probability_error", Json::real(error.max_abs_probability_error))
+        .add("mean_total_variation", Json::real(error.mean_total_variation))
+        .add("top1_agree", Json::whole(error.top1_agree));
+    Json out = Json::object();
+    out.add("dataset", Json::text(fixture_ == 0 ? "primary" : "fixture" + std::to_string(fixture_)))
+        .add("batch", Json::whole(d.batch))
+        .add("width", Json::whole(d.width))
+        .add("vocab", Json::whole(d.vocab))
+        .add("steps", Json::whole(d.steps))
+        .add("classifier_error", std::move(errors))
+        .add("tokens", std::move(tokens));
+    if (fixture_ == 0) {
+      std::fprintf(stderr, "%s: the decoder's FP32 contract check of the %s decode follows (a precision result, "
+                   "not required to pass):\n", appproto::program(), case_name(app.lowprec_case()));
+      const l2c_decoder::Expectation contract(d);
+      const bool pass = l2c_decoder::verify(
+          d, contract, {got.generated.data(), got.normalized.data(), got.logits.data(), got.probabilities.data()});
+      out.add("production_fp32_tolerance_pass", Json::flag(pass));
+    }
+    std::fprintf(stderr, "%s: accuracy of %s on %s: classifier max |error| %.3g, normalized RMS error %.3g, max "
+                 "|probability error| %.3g; %lld of %lld tokens agree\n", appproto::program(),
+                 case_name(app.lowprec_case()), fixture_ == 0 ? "the primary model" : ("fixture " + std::to_string(fixture_)).c_str(),
+                 error.max_abs_error, error.normalized_rms_error, error.max_abs_probability_error, agree,
+                 d.batch * d.steps);
+    return out;
+  }
+
+ private:
+  double median_weight_encode_ms(hipStream_t stream, int repetitions) {
+    std::vector<double> ms;
+    for (int i = 0; i < repetitions; ++i)
+      ms.push_back(ClassifierExperiment::time_ms(stream, [&] { app_->encode_weights(stream); }));
+    std::nth_element(ms.begin(), ms.begin() + repetitions / 2, ms.end());
+    return ms[static_cast<size_t>(repetitions / 2)];
+  }
+
+  ErrorMetrics classifier_error(hipStream_t stream) {
+    ClassifierExperiment &app = *app_;
+    const Dims &d = app.dims();
+    const HostModel &model = app.model();
+    std::vector<float> x(static_cast<size_t>(d.batch * d.width));
+    spread(d.batch, [&](long long b) {
+      std::vector<float> scratch;
+      rmsnorm_float(model.embedding_row(model.prompt(b), &scratch), d.width, &x[static_cast<size_t>(b * d.width)]);
     });
+    APP_HIP(hipMemcpyAsync(app.normalized(0), x.data(), x.size() * 4, hipMemcpyHostToDevice, stream));
+    app.classify(0, stream);
+    std::vector<float> device(static_cast<size_t>(d.batch * d.vocab));
+    APP_HIP(hipMemcpyAsync(device.data(), app.logits(0), device.size() * 4, hipMemcpyDeviceToHost, stream));
+    APP_HIP(hipStreamSynchronize(stream));
+    std::vector<double> reference(device.size()), actual(device.begin(), device.end());
+    spread(d.batch, [&](long long b) {
+      for (long long r = 0; r < d.vocab; ++r)
+        reference[static_cast<size_t>(b * d.vocab + r)] = model.logit(&x[static_cast<size_t>(b * d.width)], r);
+    });
+    return compare_logits(reference, actual, d.batch, d.vocab);
   }
-  long long agree = 0;
-  Json per_step = Json::list();
-  for (long long s = 0; s < S; ++s) {
-    long long n = 0;
-    for (long long b = 0; b < B; ++b) n += d.generated()[b * S + s] == expected[static_cast<size_t>(b * S + s)];
-    agree += n;
-    per_step.push(Json::whole(n));
-  }
-  Json tokens = Json::object();
-  tokens.add("agree", Json::whole(agree))
-      .add("total", Json::whole(B * S))
-      .add("per_step_agree", std::move(per_step))
-      .add("reference", Json::text(fixture == 0 ? "analytic progression" : "double host decode"));
-  Json out = Json::object();
-  out.add("dataset", Json::text(fixture == 0 ? "primary" : "fixture" + std::to_string(fixture)))
-      .add("batch", Json::whole(B))
-      .add("width", Json::whole(W))
-      .add("vocab", Json::whole(V))
-      .add("steps", Json::whole(S))
-      .add("classifier_error", metrics_json(classifier))
-      .add("tokens", std::move(tokens));
-  if (fixture == 0) {
-    const l2c_decoder::Dims dims{B, W, V, S};
-    const l2c_decoder::Expectation production(dims);
-    std::vector<float> o(dims.activation_count()), l(dims.row_count()), p(dims.row_count());
-    d.download_outputs(o.data(), l.data(), p.data());
-    std::fprintf(stderr, "%s: production FP32 tolerance check of the %s decode (reported, not required):\n",
-                 appproto::program(), case_name(c));
-    const bool pass = l2c_decoder::verify(dims, production, {d.generated(), o.data(), l.data(), p.data()});
-    out.add("production_fp32_tolerance_pass", Json::flag(pass));
-  }
-  std::fprintf(stderr, "%s: accuracy %s fixture %d: max |error| %.3g, normalized RMS %.3g, max |probability error| "
-               "%.3g, tokens %lld/%lld\n", appproto::program(), case_name(c), fixture, classifier.max_abs_error,
-               classifier.normalized_rms_error, classifier.max_abs_probability_error, agree, B * S);
-  return out;
-}
+
+  int fixture_;
+  std::unique_ptr<ClassifierExperiment> app_;
+};
 
 int run_accuracy(int c, int argc, const char *const *argv, std::string *record, bool print) {
   std::string json_out;
   for (int i = 1; i < argc; ++i) {
-    const std::string flag = argv[i];
-    if (flag == "--accuracy") continue;
-    if (flag == "--json-out" && i + 1 < argc) json_out = argv[++i];
-    else appproto::abort_run(appproto::kUsage, "--accuracy takes only --json-out PATH (got %s)", flag.c_str());
+    const std::string arg = argv[i];
+    if (arg == "--accuracy") continue;
+    if (arg == "--json-out" && i + 1 < argc) {
+      json_out = argv[++i];
+      continue;
+    }
+    appproto::abort_run(appproto::kUsage, "--accuracy takes only --json-out PATH (got %s)", arg.c_str());
   }
   hipStream_t stream;
   APP_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
   double weight_ms = 0.0;
-  appproto::Json datasets = appproto::Json::list();
+  Json datasets = Json::list();
   for (int fixture = 0; fixture <= 3; ++fixture)
-    datasets.push(accuracy_dataset(c, fixture, stream, fixture == 0 ? &weight_ms : nullptr));
+    datasets.push(Assessment(c, fixture).run(stream, fixture == 0 ? &weight_ms : nullptr));
   (void)hipStreamDestroy(stream);
-  hipDeviceProp_t prop{};
   int device = 0;
+  hipDeviceProp_t props{};
   APP_HIP(hipGetDevice(&device));
-  APP_HIP(hipGetDeviceProperties(&prop, device));
-  using appproto::Json;
+  APP_HIP(hipGetDeviceProperties(&props, device));
   Json result = Json::object();
   result.add("schema", Json::text("blackwell_experiments.lowprec_accuracy/1"))
-      .add("identity", Json::text(std::string("blackwell-experiments/lowprec-decoder-classifier/") + case_name(c)))
+      .add("identity", Json::text(identity(c)))
       .add("case", Json::text(case_name(c)))
       .add("spec_sha256", Json::text(kSpecSha256))
-      .add("device", Json::text(prop.name))
+      .add("device", Json::text(props.name))
       .add("weight_conversion_ms_median_of_5", Json::real(weight_ms))
       .add("datasets", std::move(datasets))
       .add("status", Json::text("accuracy"));
@@ -913,17 +961,17 @@ int run_accuracy(int c, int argc, const char *const *argv, std::string *record, 
   if (print) std::printf("RESULT %s\n", line.c_str());
   if (!json_out.empty()) {
     FILE *file = std::fopen(json_out.c_str(), "w");
-    if (!file || std::fprintf(file, "%s\n", line.c_str()) < 0 || std::fclose(file))
+    const bool written = file && std::fprintf(file, "%s\n", line.c_str()) >= 0;
+    if (!(file && std::fclose(file) == 0 && written))
       appproto::abort_run(appproto::kUsage, "cannot write %s", json_out.c_str());
   }
   return appproto::kPass;
 }
 
 const appproto::Provenance kBuild{"gfx950", kSpecSha256, "v1", "4a75f8d743ef7fe755822bab0ea0fb78009c145b"};
-const char kProgram[] = "decoder_lowprec";
 
-// The modes of decoder_lowprec.cu:1414-1420: --accuracy, --selftest, else the
-// loom_private protocol.
+// --accuracy and --selftest anywhere on the command line select those modes;
+// anything else is the loom_private protocol.
 int dispatch(int c, int argc, const char *const *argv, std::string *record, bool print) {
   if (c < kFp32 || c > kNvfp4) {
     std::fprintf(stderr, "lowprec: case must be 0 (fp32), 1 (bf16), 2 (mxfp6) or 3 (nvfp4) (got %d)\n", c);
@@ -931,16 +979,17 @@ int dispatch(int c, int argc, const char *const *argv, std::string *record, bool
   }
   appproto::set_program(kProgram);
   g_case = c;
+  const auto has = [&](const char *flag) {
+    return std::any_of(argv + 1, argv + argc, [&](const char *a) { return std::strcmp(a, flag) == 0; });
+  };
   try {
-    for (int i = 1; i < argc; ++i) {
-      if (std::string(argv[i]) == "--accuracy") return run_accuracy(c, argc, argv, record, print);
-      if (std::string(argv[i]) == "--selftest") return run_selftest(c);
-    }
+    if (has("--accuracy")) return run_accuracy(c, argc, argv, record, print);
+    if (has("--selftest")) return run_selftest(c);
   } catch (const appproto::Abort &a) {
     std::fprintf(stderr, "%s: %s\n", appproto::program(), a.what());
     return a.code();
   }
-  return appproto::run_protocol(kProgram, argc, argv, make_workload, kBuild, record, print);
+  return appproto::run_protocol(kProgram, argc, argv, protocol_factory, kBuild, record, print);
 }
 
 }  // namespace
