@@ -191,7 +191,7 @@ __device__ __forceinline__ void matvec_wave_row(float *out, const float *x, cons
       a3 = fmaf(m3.z, v3.z, a3); a3 = fmaf(m3.w, v3.w, a3);
     }
     for (; c < cols4; c += L2C_WAVE) {
-      const float4 m0 = ld4_stream(w4 + c);
+      const float4 m0 = NT ? ld4_stream(w4 + c) : w4[c];
       const float4 v0 = x4[c];
       a0 = fmaf(m0.x, v0.x, a0); a0 = fmaf(m0.y, v0.y, a0);
       a0 = fmaf(m0.z, v0.z, a0); a0 = fmaf(m0.w, v0.w, a0);

@@ -285,12 +285,27 @@ bool run(const Options &o, const Inputs &in, RunResult *res, std::vector<float> 
       if (o.host_write) L2C_OK(l2c_copy_to_host(dst, src, n * 4, s));
       else HIP_OK(hipMemcpyAsync(dst, src, n * 4, hipMemcpyDeviceToHost, s));
     };
+    // Kernels l2c_copy_to_host launches for one download: one over the 16-byte
+    // chunks when both pointers are 16-byte aligned, and one over the bytes
+    // left after them (the same rule the copy applies).
+    auto host_copy_kernels = [](const void *dst, const void *src, size_t bytes) {
+      const bool aligned = (reinterpret_cast<uintptr_t>(dst) % 16 == 0) && (reinterpret_cast<uintptr_t>(src) % 16 == 0);
+      const size_t chunked = aligned ? bytes / 16 * 16 : 0;
+      return (chunked > 0 ? 1 : 0) + (chunked < bytes ? 1 : 0);
+    };
     // Kernels one iteration launches (the block-scaled products launch their
-    // activation quantizer too; hostwrite adds one kernel per download).
+    // activation quantizer too; hostwrite adds the copy kernels of the three
+    // downloads).
     const int kernels_per_rep = mm == Matmul::kFused ? 1 : 3 + (scaled ? 1 : 0);
+    const int host_write_kernels =
+        o.copy_outputs && o.host_write
+            ? host_copy_kernels(h_normalized.ptr, d_normalized.ptr, vec_elems * 4) +
+                  host_copy_kernels(h_softmax.ptr, d_softmax.ptr, vec_elems * 4) +
+                  host_copy_kernels(h_product.ptr, d_product.ptr, prod_elems * 4)
+            : 0;
     const int kernels_per_iter_planned =
-        kernels_per_rep * o.repeats +
-        (o.copy_outputs ? (o.host_write ? 3 : 0) + (mm == Matmul::kFused && !o.one_stream ? 1 : 0) : 0);
+        kernels_per_rep * o.repeats + host_write_kernels +
+        (o.copy_outputs ? (mm == Matmul::kFused && !o.one_stream ? 1 : 0) : 0);
 
     // One iteration. Three-stream variants: fork from the product's stream,
     // `repeats` x {rmsnorm | softmax | matmul} on their streams, copies on
