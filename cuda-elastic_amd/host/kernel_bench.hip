@@ -19,10 +19,16 @@
 // counters.
 //
 // `gemv_cold` times the coalesced matrix-vector product with the 256 MB
-// Infinity Cache (MALL) flushed before every launch: a copy of 1 GiB runs
-// between launches and only the product is bracketed by events, so its time
-// is HBM's rate for W, not a MALL hit's (`gemv` runs back to back, where a W
-// of up to ~256 MB stays in the MALL between launches).
+// Infinity Cache (MALL) flushed before every launch by a read-only sweep of
+// 1 GiB (ordinary loads, nothing written), so no dirty line is left to be
+// written back while the product is timed; only the product is bracketed by
+// events, so its time is HBM's rate for W, not a MALL hit's (`gemv` runs back
+// to back, where a W of up to ~256 MB stays in the MALL between launches).
+// `gemv_cold_copy` flushes with a 1 GiB copy instead (512 MiB read, 512 MiB
+// written), the form that leaves dirty lines behind. `read_cold` times the
+// read-only sweep kernel itself over W's bytes after the same flush: a plain
+// streaming read of that many bytes from HBM, the rate an isolated product of
+// that size can hope for.
 //
 // `vendor_f32` and `vendor_bf16` time the vendor library's GEMM of the same
 // contraction (hipBLASLt, out[b][r] = sum_k X[b][k] W[r][k] with fp32 or bf16
@@ -83,6 +89,19 @@ __global__ void copy_kernel(float4 *dst, const float4 *src, size_t n4) {
   const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
   for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride)
     dst[i] = src[i];
+}
+
+// Reads n4 float4s with ordinary (allocating) loads and writes nothing unless
+// their sum is exactly `never` (the inputs are finite and the caller passes a
+// value no sum reaches), so the loads cannot be dropped and no line is dirtied.
+__global__ void sweep_kernel(const float4 *src, size_t n4, float never, float *sink) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  float acc = 0.0f;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    const float4 v = src[i];
+    acc += (v.x + v.y) + (v.z + v.w);
+  }
+  if (acc == never) sink[0] = acc;
 }
 
 // Fills n floats with a deterministic pattern in [-1, 1) scaled by `scale`.
@@ -617,28 +636,49 @@ int main(int argc, char **argv) {
   hipEvent_t t0, t1;
   CHECK(hipEventCreate(&t0));
   CHECK(hipEventCreate(&t1));
-  if (op == "gemv_cold") {
-    constexpr size_t kFlush = size_t(512) << 20;  // two 512 MiB buffers: 1 GiB moved per flush
+  if (op == "gemv_cold" || op == "gemv_cold_copy" || op == "read_cold") {
+    constexpr size_t kFlush = size_t(1) << 30;  // 1 GiB: four times the MALL
     float4 *fa = nullptr, *fb = nullptr;
+    float *sink = nullptr;
     CHECK(hipMalloc(&fa, kFlush));
-    CHECK(hipMalloc(&fb, kFlush));
+    CHECK(hipMalloc(&sink, 4));
     CHECK(hipMemset(fa, 0, kFlush));
-    double total_ms = 0.0;
-    for (int i = 0; i < iters + 3; ++i) {
-      hipLaunchKernelGGL(copy_kernel, dim3(4096), dim3(256), 0, s, fb, fa, kFlush / 16);
+    const bool copy_flush = op == "gemv_cold_copy";
+    if (copy_flush) CHECK(hipMalloc(&fb, kFlush / 2));
+    // The flush: a read of 1 GiB, or a copy of 512 MiB into another 512 MiB.
+    auto flush = [&]() {
+      if (copy_flush)
+        hipLaunchKernelGGL(copy_kernel, dim3(4096), dim3(256), 0, s, fb, fa, kFlush / 2 / 16);
+      else
+        hipLaunchKernelGGL(sweep_kernel, dim3(4096), dim3(256), 0, s, fa, kFlush / 16, -1.0f, sink);
       CHECK(hipGetLastError());
+    };
+    double total_ms = 0.0, flush_ms = 0.0;
+    hipEvent_t f0;
+    CHECK(hipEventCreate(&f0));
+    for (int i = 0; i < iters + 3; ++i) {
+      CHECK(hipEventRecord(f0, s));
+      flush();
       CHECK(hipEventRecord(t0, s));
-      L2C(l2c_matvec(prod, x, m, S, R, L2C_MATVEC_COALESCED, s));
+      if (op == "read_cold")
+        hipLaunchKernelGGL(sweep_kernel, dim3(4096), dim3(256), 0, s, reinterpret_cast<const float4 *>(m), mat / 4,
+                           1.0e30f, sink);
+      else
+        L2C(l2c_matvec(prod, x, m, S, R, L2C_MATVEC_COALESCED, s));
+      CHECK(hipGetLastError());
       CHECK(hipEventRecord(t1, s));
       CHECK(hipEventSynchronize(t1));
-      float ms = 0.0f;
+      float ms = 0.0f, fms = 0.0f;
       CHECK(hipEventElapsedTime(&ms, t0, t1));
-      if (i >= 3) total_ms += ms;  // three untimed rounds first
+      CHECK(hipEventElapsedTime(&fms, f0, t0));
+      if (i >= 3) total_ms += ms, flush_ms += fms;  // three untimed rounds first
     }
     const double us = 1000.0 * total_ms / iters;
-    const double bytes = mat * 4.0 + (S + static_cast<double>(R)) * 4;
-    std::printf("op=%s batch=%d size=%d rows=%d iters=%d avg_us=%.3f bytes=%.0f gbps=%.1f\n", op.c_str(), B, S, R,
-                iters, us, bytes, bytes / (us * 1e3));
+    const double bytes = op == "read_cold" ? mat * 4.0 : mat * 4.0 + (S + static_cast<double>(R)) * 4;
+    std::printf("op=%s batch=%d size=%d rows=%d iters=%d avg_us=%.3f bytes=%.0f gbps=%.1f flush=%s flush_us=%.1f\n",
+                op.c_str(), B, S, R, iters, us, bytes, bytes / (us * 1e3), copy_flush ? "copy_512MiB" : "read_1GiB",
+                1000.0 * flush_ms / iters);
+    CHECK(hipEventDestroy(f0));
     return 0;
   }
   // Warm-up of 100 ms (at least 3 and at most 1000 launches): the matrix cores reach their

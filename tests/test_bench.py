@@ -84,6 +84,7 @@ def test_full_plan_result_line_fits_the_driver(monkeypatch):
 
     monkeypatch.setattr(l2c, "load_host", lambda: None)
     monkeypatch.setattr(bench, "run_line", lambda lib, args: _harness_record(args))
+    monkeypatch.setattr(bench, "run_line_child", lambda lib, args, env: _harness_record(args))
     monkeypatch.setattr(bench, "decoder_line", lambda lib, mode: {
         "name": f"decoder_large_{mode}", "mode": mode, "batch": 1024, "width": 16384, "vocab": 8192, "steps": 4,
         "iterations": 10, "warmup": 3, "compute_us_per_invocation": 7654.321987,
@@ -112,6 +113,7 @@ def test_full_plan_result_line_fits_the_driver(monkeypatch):
     print("result line length", len(printed[0]))
     d = json.loads(printed[0])
     names = ["c4_batched_graph_nocopy"] + [n for n, _ in bench.full_plan(50, 100)] + \
+        [n for n, _, _ in bench.child_plan(50, 100)] + \
         ["decoder_large_graph", "decoder_large_direct"] + [f"lowprec_{c}_graph" for c in
                                                            ("fp32", "bf16", "mxfp6", "nvfp4")]
     assert len(names) == len(set(names)) >= 55

@@ -97,3 +97,32 @@ def test_check_and_compare_plans():
         assert [c.label for c in g] == ["graph", "direct", "fused", "naive"]
         assert len({(c.batch, c.size, c.rows, c.inputs, c.copies) for c in g}) == 1
     assert groups[0][0].argv("/tmp/x.bin")[-1] == "--dump=/tmp/x.bin"
+
+
+def test_launch_trace_summary_on_a_synthetic_trace(tmp_path):
+    """l2c.launch_trace on a trace whose figures are known: 8 graph launches
+    of 20 us host time each, one 3 us kernel per launch starting 5 us after
+    the call returns, one launch every 20 us."""
+    from l2c import launch_trace
+
+    api, kernels = [], []
+    for i in range(8):
+        t0 = 1_000_000 + i * 20_000
+        api.append({"Function": "hipGraphLaunch", "Correlation_Id": str(i), "Start_Timestamp": str(t0),
+                    "End_Timestamp": str(t0 + 20_000)})
+        k0 = t0 + 25_000
+        kernels.append({"Kernel_Name": "fused_kernel", "Correlation_Id": str(i), "Start_Timestamp": str(k0),
+                        "End_Timestamp": str(k0 + 3_000)})
+    d = tmp_path / "trace" / "host"
+    d.mkdir(parents=True)
+    for name, rows in (("t_hip_api_trace.csv", api), ("t_kernel_trace.csv", kernels)):
+        with open(d / name, "w", newline="") as f:
+            w = csv.DictWriter(f, fieldnames=list(rows[0]))
+            w.writeheader()
+            w.writerows(rows)
+    s = launch_trace.summarize_dir(str(tmp_path / "trace"))
+    assert s["api"]["hipGraphLaunch"] == {"n": 8, "mean_us": 20.0, "median_us": 20.0}
+    assert s["kernels"]["fused_kernel"] == {"n": 8, "mean_us": 3.0}
+    assert s["steady"]["kernels"] == 4 and s["steady"]["gap_median_us"] == 17.0
+    assert s["steady"]["busy_frac"] == round(12.0 / 63.0, 3)
+    assert s["call_end_to_kernel_start_us"]["hipGraphLaunch"]["median"] == 5.0
