@@ -425,6 +425,231 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_kernel(float *__restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// The MXFP4 contraction on wide tiles: 128 (batch) x 256 (rows) x 128 (k per
+// step). The staging of both operands goes through the same L2 -> LDS DMA
+// return path, and the block-scaled kernels are bound by it: their time tracks
+// the number of LDS-DMA instructions (about 35 return-path cycles each per CU,
+// `TD_TD_BUSY` 0.86 of the cycles on the 256 x 128 tile). Per 64 MFMAs this
+// tile issues 34 DMA instructions against 43: X codes 16 KB (16 one-KB
+// instructions), W codes 16 KB (16), the X scale words (1) and the W scales
+// (1). The W scales are staged 16 bytes a row, the scale words of four
+// consecutive steps (row-major [rows][cols / 32] bytes, so four steps of one
+// row are contiguous), into a three-slot ring: the DMA of step t carries part
+// (t + 5) % 4 (rows 64 part .. 64 part + 63) of the four-step group
+// (t + 5) / 4, so a group's four parts are issued by step 4 G - 2 and have
+// landed, by the one-step-ahead wait, before its first reader at step 4 G;
+// the slot a group refills was last read at step 4 G - 9. Needs
+// cols % 512 == 0 (whole four-step groups, 16-byte aligned scale rows).
+//
+// Waves: p = wave & 3 takes the 64 x 128 output sub-tile (wm = p & 1 of the
+// batch rows, wn = p >> 1 of the weight rows), 2 x 4 blocks of 32 x 32; wave
+// group g = wave >> 2 takes the k-slice [64 g, 64 g + 64) of every step, as in
+// scaled_gemm_kernel, whose ping-pong schedule, fragment placement and
+// swizzles this kernel keeps. Fragment reads per wave and step: 4 + 4 of 16
+// bytes, 2 + 4 scale words.
+constexpr int kWideBM = 128;
+constexpr int kWideBN = 256;
+constexpr int kWideXBytes = kWideBM * kBK;                  // 16 KB of X codes
+constexpr int kWideWBytes = kWideBN * 64;                   // 16 KB of E2M1 codes
+constexpr int kWideXS = kWideXBytes + kWideWBytes;          // X scale words (1 KB DMA, 512 B used)
+constexpr int kWideStage = kWideXS + 1024;
+constexpr int kWideRing = kStages * kWideStage;             // W scale ring: 3 x 256 rows x 16 B
+constexpr int kWideRingSlot = kWideBN * 16;
+constexpr int kWideLds = kWideRing + 3 * kWideRingSlot > kExchange ? kWideRing + 3 * kWideRingSlot : kExchange;
+static_assert(kWideLds <= 160 * 1024, "the wide tile's stages fit the LDS");
+
+__global__ __launch_bounds__(kThreads, 1) void scaled_gemm_wide_kernel(float *__restrict__ out,
+                                                                     const uint8_t *__restrict__ Xc,
+                                                                     const uint8_t *__restrict__ Xs,
+                                                                     const uint8_t *__restrict__ Wq,
+                                                                     const uint8_t *__restrict__ Ws, int M,
+                                                                     int N, int K) {
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[kWideLds];
+  int tile = blockIdx.x;
+  const int tiles = gridDim.x;
+  if (tiles % kXcds == 0) tile = (tile % kXcds) * (tiles / kXcds) + tile / kXcds;
+  const int mtiles = (M + kWideBM - 1) / kWideBM;
+  const int m0 = (tile % mtiles) * kWideBM, n0 = (tile / mtiles) * kWideBN;
+  const int mrows = min(kWideBM, M - m0), nrows = min(kWideBN, N - n0);
+  const int Mp = padded4(M);
+  const int tid = threadIdx.x, lane = tid % L2C_WAVE;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / L2C_WAVE);
+  const int g = wave >> 2, p = wave & 3;
+  const int wm = p & 1, wn = p >> 1;
+  const int r = lane % 32, h = lane / 32;
+  const int steps = K / kBK;
+  const int groups = steps / 4;
+  const int wrb = K / 2;   // E2M1 code bytes per row
+  const int srb = K / 32;  // scale bytes per row
+  const __amdgpu_buffer_rsrc_t rx =
+      l2c::buffer_rsrc(Xc + static_cast<size_t>(m0) * K, static_cast<uint32_t>(mrows) * K);
+  const __amdgpu_buffer_rsrc_t rxs = l2c::buffer_rsrc(Xs, static_cast<uint32_t>(Mp) * 4 * steps);
+  const __amdgpu_buffer_rsrc_t rw =
+      l2c::buffer_rsrc(Wq + static_cast<size_t>(n0) * wrb, static_cast<uint32_t>(nrows) * wrb);
+  const __amdgpu_buffer_rsrc_t rws =
+      l2c::buffer_rsrc(Ws + static_cast<size_t>(n0) * srb, static_cast<uint32_t>(nrows) * srb);
+
+  // Per-lane DMA sources. X: instruction 8 k + wave (k < 2) fills rows
+  // 8 (8 k + wave) + lane / 8, slot lane % 8 with chunk slot ^ xswizzle(row).
+  // W: instruction 8 k + wave fills rows 16 (8 k + wave) + lane / 4, slot
+  // lane % 4 with chunk slot ^ ((row >> 2) & 3). X scales (wave 4): rows
+  // 4 lane .. 4 lane + 3 (lanes past the tile read the last rows again into
+  // the unused half). W scales (wave 5): row 64 part + lane.
+  int xsrc[2], wsrc[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int xrow = 8 * (8 * k + wave) + lane / 8;
+    xsrc[k] = min(xrow, mrows - 1) * K + 16 * ((lane % 8) ^ xswizzle(xrow));
+    const int wrow = 16 * (8 * k + wave) + lane / 4;
+    wsrc[k] = min(wrow, nrows - 1) * wrb + 16 * ((lane % 4) ^ ((wrow >> 2) & 3));
+  }
+  const int xssrc = min(16 * lane, (Mp - m0) * 4 - 16);
+
+  // The W scale part u (group u / 4, rows 64 (u % 4) + lane) into its ring
+  // slot; groups past the last re-read the last group into a slot no step
+  // reads any more.
+  auto scale_dma = [&](int u) __attribute__((always_inline)) {
+    const int part = u & 3, group = min(u >> 2, groups - 1);
+    const int row = min(64 * part + lane, nrows - 1);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rws, (lds_ptr *)(lds + kWideRing + ((u >> 2) % 3) * kWideRingSlot + 64 * part * 16), 16, row * srb,
+        16 * group, 0, 0);
+  };
+  auto dma = [&](int stage, int t, int u) __attribute__((always_inline)) {
+    unsigned char *base = lds + stage * kWideStage;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr *)(base + (8 * k + wave) * 1024), 16, xsrc[k], kBK * t,
+                                               0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + kWideXBytes + (8 * k + wave) * 1024), 16,
+                                               wsrc[k], 64 * t, 0, 0);
+    }
+    if (wave == 4)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rxs, (lds_ptr *)(base + kWideXS), 16, xssrc, Mp * 4 * t + m0 * 4, 0,
+                                               0);
+    if (wave == 5) scale_dma(u);
+  };
+  // This wave's DMA of the older of two outstanding steps has landed (4
+  // instructions a step, 5 on waves 4 and 5) and its LDS reads are done;
+  // then the workgroup barrier.
+  auto wait_dma_barrier = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (wave == 4 || wave == 5)
+      asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto barrier = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Fragments of lane (r, h) for the instruction over the step's blocks 2 g
+  // and 2 g + 1: X rows wm * 64 + 32 i + r, chunks 4 g + h and 4 g + 2 + h; W
+  // rows wn * 128 + 32 j + r, chunk 2 g + h; scale byte 2 g + h of each row's
+  // step word (X from the stage, W from the ring slot of the step's group).
+  const int blk = 2 * g + h;
+  const int xsw = xswizzle(r);
+  const int xa = (wm * 64 + r) * 128;
+  const int xc0 = 16 * ((4 * g + h) ^ xsw), xc1 = 16 * ((4 * g + 2 + h) ^ xsw);
+  const int wr0 = wn * 128 + r;
+  const int wa = kWideXBytes + wr0 * 64 + 16 * (blk ^ ((r >> 2) & 3));
+  const int shift = 8 * blk;
+  u32x4 fa[2][2], fb[4];
+  unsigned sa[2], sb[4];
+  auto read = [&](int stage, int t) __attribute__((always_inline)) {
+    const unsigned char *base = lds + stage * kWideStage;
+    const unsigned char *ring = lds + kWideRing + ((t >> 2) % 3) * kWideRingSlot + (t & 3) * 4;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      fa[i][0] = *reinterpret_cast<const u32x4 *>(base + xa + 4096 * i + xc0);
+      fa[i][1] = *reinterpret_cast<const u32x4 *>(base + xa + 4096 * i + xc1);
+      sa[i] = *reinterpret_cast<const unsigned *>(base + kWideXS + (wm * 64 + 32 * i + r) * 4) >> shift;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      fb[j] = *reinterpret_cast<const u32x4 *>(base + wa + 32 * 64 * j);
+      sb[j] = *reinterpret_cast<const unsigned *>(ring + (wr0 + 32 * j) * 16) >> shift;
+    }
+  };
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // Prologue: W scale parts 0-2 of group 0 (wave 5), then steps 0 and 1 with
+  // parts 3 and 4; the wait leaves only step 1's DMA outstanding.
+  const int last = steps - 1;
+  if (wave == 5) {
+    scale_dma(0);
+    scale_dma(1);
+    scale_dma(2);
+  }
+  dma(0, 0, 3);
+  dma(1, min(1, last), 4);
+  wait_dma_barrier();
+  if (g == 1) barrier();
+  int cur = 0;
+  for (int t = 0; t < steps; ++t) {
+    dma(cur == 0 ? kStages - 1 : cur - 1, min(t + 2, last), t + 5);
+    read(cur, t);
+    wait_dma_barrier();
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      i32x8 a;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) a[c] = static_cast<int>(fa[i][0][c]), a[4 + c] = static_cast<int>(fa[i][1][c]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        i32x8 b;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) b[c] = static_cast<int>(fb[j][c]), b[4 + c] = 0;
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc[i][j], kFmtE4M3, kFmtE2M1, 0,
+                                                                    static_cast<int>(sa[i]), 0,
+                                                                    static_cast<int>(sb[j]));
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    barrier();
+    cur = cur == kStages - 1 ? 0 : cur + 1;
+  }
+  if (g == 0) barrier();
+
+  // Partial sums of the two k-slices: group 1 stores, group 0 adds and writes.
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  float *exchange = reinterpret_cast<float *>(lds);
+  if (g == 1) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) exchange[((p * 8 + i * 4 + j) * 16 + v) * L2C_WAVE + lane] = acc[i][j][v];
+  }
+  __syncthreads();
+  if (g == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = wn * 128 + 32 * j + r;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int m = wm * 64 + 32 * i + 8 * (v / 4) + 4 * h + v % 4;
+          const float sum = acc[i][j][v] + exchange[((p * 8 + i * 4 + j) * 16 + v) * L2C_WAVE + lane];
+          if (m < mrows && n < nrows) __builtin_nontemporal_store(sum, &out[static_cast<size_t>(m0 + m) * N + n0 + n]);
+        }
+    }
+  }
+}
+
 // Workspace views.
 struct Mxfp8View {
   uint8_t *codes;
@@ -486,7 +711,15 @@ extern "C" int l2c_matmul_qs(float *out, const void *Xbf16, const void *Wq, cons
   const Mxfp8View v = view(workspace, batch, cols);
   if (const int e = launch_quantizer(v, static_cast<const uint16_t *>(Xbf16), batch, cols, stream)) return e;
   const uint8_t *W = static_cast<const uint8_t *>(Wq);
-  if (fmt == L2C_Q_MXFP4)
+  // Wide tiles for MXFP4 weights in whole four-step scale groups whose 16-byte
+  // scale rows are aligned; the 256 x 128 tile otherwise.
+  const long long wide_tiles =
+      static_cast<long long>((batch + kWideBM - 1) / kWideBM) * ((rows + kWideBN - 1) / kWideBN);
+  if (fmt == L2C_Q_MXFP4 && cols % 512 == 0 && l2c_aligned16(scales) &&
+      static_cast<long long>(kWideBN) * (cols / 2) <= 0x7fffffffLL && wide_tiles <= 0x7fffffffLL) {
+    hipLaunchKernelGGL(scaled_gemm_wide_kernel, dim3(static_cast<unsigned>(wide_tiles)), dim3(kThreads), 0, stream,
+                       out, v.codes, v.scales, W, static_cast<const uint8_t *>(scales), batch, rows, cols);
+  } else if (fmt == L2C_Q_MXFP4)
     hipLaunchKernelGGL(scaled_gemm_kernel<L2C_Q_MXFP4>, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream,
                        out, v.codes, v.scales, W, scales, batch, rows, cols);
   else

@@ -9,7 +9,9 @@
 //   OP: rmsnorm softmax gemv naive fused matmul mxfp4 fp8 copy vendor_f32 vendor_bf16
 //       mxfp4s fp8s (the block-scaled product: MXFP8 activation quantizer +
 //       scaled contraction, as l2c_matmul_qs runs them; cvt_mxfp8 the
-//       quantizer alone)
+//       quantizer alone; mxfp4s_narrow the same MXFP4 product with the scale
+//       array 4 bytes past a 16-byte boundary, which l2c_matmul_qs runs on its
+//       256 x 128 tile instead of the 128 x 256 one)
 //       bf16 mxfp6 (lowprec classifier contractions, alpha on for bf16)
 //       cvt_bf16 cvt_mxfp6 cvt_nvfp4 (lowprec per-step activation conversions
 //       of BATCH x SIZE; cvt_nvfp4 = tensor scales + codes + bf16 expansion)
@@ -526,7 +528,8 @@ int main(int argc, char **argv) {
       L2C(l2c_quantize_mxfp6(codes, sc8, m, R, S, nullptr));
     }
   }
-  const bool scaled = op == "mxfp4s" || op == "fp8s" || op == "cvt_mxfp8";
+  const bool narrow = op == "mxfp4s_narrow";
+  const bool scaled = op == "mxfp4s" || op == "fp8s" || op == "cvt_mxfp8" || narrow;
   if (scaled) {
     ws_bytes = l2c_mxfp8_workspace_bytes(B, S);
     if (ws_bytes == 0) {
@@ -542,9 +545,12 @@ int main(int argc, char **argv) {
     }
     CHECK(hipMalloc(&xb, vec * 2));
     L2C(l2c_to_bf16(xb, x, vec, nullptr));
-    if (op == "mxfp4" || op == "mxfp4s") {
+    if (op == "mxfp4" || op == "mxfp4s" || narrow) {
       CHECK(hipMalloc(&codes, mat / 2));
-      CHECK(hipMalloc(&sc8, mat / 32));
+      // narrow: the scales start 4 bytes into their allocation (4-byte
+      // aligned, as the C ABI requires, but not 16-byte aligned).
+      CHECK(hipMalloc(&sc8, mat / 32 + (narrow ? 4 : 0)));
+      if (narrow) sc8 += 4;
       L2C(l2c_quantize_mxfp4(codes, sc8, m, R, S, nullptr));
     } else {
       CHECK(hipMalloc(&codes, mat));
@@ -588,8 +594,8 @@ int main(int argc, char **argv) {
       bytes = vec * 2.0 + (op == "mxfp4" ? mat / 2.0 + mat / 32.0 : mat + R * 4.0) +
               static_cast<double>(B) * R * 4;
       flops = 2.0 * B * static_cast<double>(mat);
-    } else if (op == "mxfp4s" || op == "fp8s") {
-      const bool mx = op == "mxfp4s";
+    } else if (op == "mxfp4s" || op == "fp8s" || narrow) {
+      const bool mx = op != "fp8s";
       L2C(l2c_matmul_qs(prod, xb, codes, mx ? static_cast<const void *>(sc8) : sc32, mx ? L2C_Q_MXFP4 : L2C_Q_FP8, B,
                         S, R, ws, ws_bytes, s));
       bytes = vec * 2.0 + (mx ? mat / 2.0 + mat / 32.0 : mat + R * 4.0) + static_cast<double>(B) * R * 4;

@@ -107,10 +107,14 @@ def check_qs(torch, l2c, orc, fmt, batch, size, rows, x, W, label):
 @pytest.mark.parametrize("fmt", [0, 1])
 # One k-step (128), two, three (as many as the DMA ring has stages), ragged
 # tiles on both axes, batches that are not a multiple of 4 (padded scale
-# rows), and grids of many tiles with the XCD-ordered tile map.
+# rows), and grids of many tiles with the XCD-ordered tile map. MXFP4 weights
+# with size % 512 == 0 take the 128 x 256 tile with its four-step scale ring:
+# one scale group (512), exactly as many groups as ring slots (1536), ragged
+# tiles on both axes past one tile (600 and 513 rows, 130 and 257 vectors).
 @pytest.mark.parametrize("batch,size,rows", [(8, 128, 16), (5, 128, 9), (3, 256, 5), (9, 384, 17),
                                              (300, 1024, 200), (33, 384, 77), (256, 4096, 256),
-                                             (520, 1152, 1030), (1024, 2048, 1024)])
+                                             (520, 1152, 1030), (1024, 2048, 1024), (5, 512, 9),
+                                             (130, 1536, 600), (257, 2560, 513)])
 def test_matmul_qs(torch_gpu, l2c, orc, fmt, batch, size, rows):
     inp = orc.fill("normal", 6, batch, size, rows)
     check_qs(torch_gpu, l2c, orc, fmt, batch, size, rows, inp.input, inp.matrix, "normal")
