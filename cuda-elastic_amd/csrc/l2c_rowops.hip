@@ -414,7 +414,7 @@ int l2c_gemm_launch_shape(int batch, int cols, int rows, int *grid, int *block,
                           int *blocks_per_cu);
 int l2c_qgemm_launch_shape(int fmt, int batch, int cols, int rows, int *grid, int *block,
                            int *blocks_per_cu);
-int l2c_scgemm_occupancy(int fmt, int *blocks_per_cu);
+int l2c_scgemm_occupancy(int fmt, bool wide, int *blocks_per_cu);
 
 extern "C" int l2c_launch_shape(int op, int batch, int cols, int rows, int variant, int *grid,
                                 int *block, int *blocks_per_cu) {
@@ -463,11 +463,15 @@ extern "C" int l2c_launch_shape(int op, int batch, int cols, int rows, int varia
       return l2c_gemm_launch_shape(batch, cols, rows, grid, block, blocks_per_cu);
     case L2C_OP_MATMUL_Q:
       return l2c_qgemm_launch_shape(variant, batch, cols, rows, grid, block, blocks_per_cu);
-    case L2C_OP_MATMUL_QS:
+    case L2C_OP_MATMUL_QS: {
       if (variant != L2C_Q_MXFP4 && variant != L2C_Q_FP8) return hipErrorInvalidValue;
-      *grid = ((batch + 255) / 256) * ((rows + 127) / 128);
+      // MXFP4 with cols % 512 == 0 runs on 128 x 256 tiles (for a 16-byte
+      // aligned scale array, as the harness's is), the rest on 256 x 128.
+      const bool wide = variant == L2C_Q_MXFP4 && cols % 512 == 0;
+      *grid = wide ? ((batch + 127) / 128) * ((rows + 255) / 256) : ((batch + 255) / 256) * ((rows + 127) / 128);
       *block = 512;
-      return l2c_scgemm_occupancy(variant, blocks_per_cu);
+      return l2c_scgemm_occupancy(variant, wide, blocks_per_cu);
+    }
     default:
       return hipErrorInvalidValue;
   }

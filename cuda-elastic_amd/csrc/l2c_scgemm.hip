@@ -766,8 +766,9 @@ extern "C" int l2c_matmul_qs_static(float *out, const void *Xbf16, const void *W
   return l2c_matmul_qs(out, Xbf16, Wq, scales, fmt, batch, cols, rows, ws, L2C_QS_STATIC_SCRATCH_BYTES, stream);
 }
 
-int l2c_scgemm_occupancy(int fmt, int *blocks_per_cu) {
-  const void *fn = fmt == L2C_Q_MXFP4 ? reinterpret_cast<const void *>(scaled_gemm_kernel<L2C_Q_MXFP4>)
-                                      : reinterpret_cast<const void *>(scaled_gemm_kernel<L2C_Q_FP8>);
+int l2c_scgemm_occupancy(int fmt, bool wide, int *blocks_per_cu) {
+  const void *fn = wide ? reinterpret_cast<const void *>(scaled_gemm_wide_kernel)
+                   : fmt == L2C_Q_MXFP4 ? reinterpret_cast<const void *>(scaled_gemm_kernel<L2C_Q_MXFP4>)
+                                        : reinterpret_cast<const void *>(scaled_gemm_kernel<L2C_Q_FP8>);
   return static_cast<int>(hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, kThreads, 0));
 }

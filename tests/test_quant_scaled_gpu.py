@@ -188,3 +188,13 @@ def test_quantize_mxfp8_every_bf16_value(torch_gpu, l2c, orc, shift):
     bad = np.flatnonzero(got != oc)
     assert bad.size == 0, (bad[:8], x[bad[:8]], got[bad[:8]], oc[bad[:8]])
     np.testing.assert_array_equal(untile_scales(tiled.cpu().numpy(), rows, cols)[0].reshape(-1), osc)
+
+
+def test_launch_shape_names_the_tile_the_product_runs(torch_gpu, l2c):
+    """l2c_launch_shape reports the 128 x 256 grid for MXFP4 products with
+    cols % 512 == 0 and the 256 x 128 grid otherwise (and for fp8)."""
+    assert l2c.launch_shape(l2c.OP_MATMUL_QS, 300, 1024, 600, l2c.Q_MXFP4)[:2] == (3 * 3, 512)
+    assert l2c.launch_shape(l2c.OP_MATMUL_QS, 300, 1152, 600, l2c.Q_MXFP4)[:2] == (2 * 5, 512)
+    assert l2c.launch_shape(l2c.OP_MATMUL_QS, 300, 1024, 600, l2c.Q_FP8)[:2] == (2 * 5, 512)
+    assert l2c.launch_shape(l2c.OP_MATMUL_QS, 1024, 16384, 8192, l2c.Q_MXFP4)[:2] == (256, 512)
+    assert l2c.launch_shape(l2c.OP_MATMUL_QS, 1024, 16384, 8192, l2c.Q_MXFP4)[2] == 1
