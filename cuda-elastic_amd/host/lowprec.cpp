@@ -412,9 +412,11 @@ class ClassifierExperiment final : public appproto::Application {
 
   bool outputs_match() override;
 
+  // The generated tokens as the last application-scope invocation downloaded
+  // them, then whatever the last check read back (nothing outside a check).
   uint64_t outputs_digest() const override {
     appproto::Digest h;
-    h.add(last_.generated.data(), last_.generated.size() * sizeof(int))
+    h.add(pinned_generated_.get(), d_.token_count() * sizeof(int))
         .add(last_.normalized.data(), last_.normalized.size() * 4)
         .add(last_.logits.data(), last_.logits.size() * 4)
         .add(last_.probabilities.data(), last_.probabilities.size() * 4)
