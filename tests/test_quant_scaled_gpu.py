@@ -198,3 +198,30 @@ def test_launch_shape_names_the_tile_the_product_runs(torch_gpu, l2c):
     assert l2c.launch_shape(l2c.OP_MATMUL_QS, 300, 1024, 600, l2c.Q_FP8)[:2] == (2 * 5, 512)
     assert l2c.launch_shape(l2c.OP_MATMUL_QS, 1024, 16384, 8192, l2c.Q_MXFP4)[:2] == (256, 512)
     assert l2c.launch_shape(l2c.OP_MATMUL_QS, 1024, 16384, 8192, l2c.Q_MXFP4)[2] == 1
+
+
+@pytest.mark.parametrize("batch,cols,rows", [(130, 1536, 600), (1024, 16384, 1024)])
+def test_wide_and_narrow_mxfp4_tiles_agree_bit_for_bit(torch_gpu, l2c, orc, batch, cols, rows):
+    """MXFP4 products with cols % 512 == 0 run on the 128 x 256 tile when the
+    scale array is 16-byte aligned and on the 256 x 128 tile otherwise; every
+    output accumulates the same MFMA sequence in both, so the two agree bit for
+    bit. The second call reads a copy of the scales 4 bytes past a 16-byte
+    boundary (4-byte aligned, as the C ABI requires)."""
+    torch = torch_gpu
+    print(f"case wide/narrow mxfp4s {batch}x{cols}x{rows}", flush=True)
+    inp = orc.fill("normal", 9, batch, cols, rows)
+    codes, scales = weights(torch, l2c, 0, inp.matrix, rows, cols)
+    xbf = bf16_activations(torch, l2c, inp.input)
+    ws = torch.empty(l2c.mxfp8_workspace_bytes(batch, cols), dtype=torch.uint8, device="cuda")
+    wide = torch.full((batch * rows,), float("nan"), dtype=torch.float32, device="cuda")
+    narrow = torch.full((batch * rows,), float("nan"), dtype=torch.float32, device="cuda")
+    holder = torch.zeros(scales.numel() + 16, dtype=torch.uint8, device="cuda")
+    shifted = holder[4:4 + scales.numel()]
+    shifted.copy_(scales)
+    assert scales.data_ptr() % 16 == 0 and shifted.data_ptr() % 16 == 4
+    l2c.matmul_qs(wide, xbf, codes, scales, 0, batch, cols, rows, ws)
+    l2c.matmul_qs(narrow, xbf, codes, shifted, 0, batch, cols, rows, ws)
+    torch.cuda.synchronize()
+    w, n = wide.cpu().numpy(), narrow.cpu().numpy()
+    assert np.isfinite(w).all()
+    np.testing.assert_array_equal(w.view(np.uint32), n.view(np.uint32))
