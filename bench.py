@@ -260,9 +260,10 @@ def plan_args(mode, launches, batch, size, rows, copies, matmul, inputs="scaled=
 
 
 def full_plan(K, W):
-    """(name, argv) of every harness line after the headline: the graph /
-    direct and copy / nocopy splits of C2, C3 and C4, the fused launch, the
-    one-stream and host-write iteration forms, and the four C5 formats."""
+    """(name, argv) of every harness line after the headline: the C1 smoke
+    shape, the graph / direct and copy / nocopy splits of C2, C3 and C4, the
+    fused launch, the one-stream and host-write iteration forms, and the four
+    C5 formats."""
     B, S, R = B_C4, S_C4, R_C4
     c2 = (1, 4096, 11008)
     c3 = (8, 768, 2048)
@@ -271,7 +272,11 @@ def full_plan(K, W):
         return plan_args(mode, launches, *shape, copies, matmul, inputs=inputs, warm=warm, extra=extra)
 
     c4 = (B, S, R)
+    c1 = (1, 288, 288)
     plan = [
+        ("c1_graph_nocopy", cfg("graph", 10000, c1, "nocopy", "coalesced", warm=100)),
+        ("c1_direct_nocopy", cfg("direct", 10000, c1, "nocopy", "coalesced", warm=100)),
+        ("c1_fused_direct_nocopy", cfg("direct", 10000, c1, "nocopy", "fused", warm=100)),
         ("c4_batched_direct_nocopy", cfg("direct", K, c4, "nocopy", "batched")),
         ("c4_batched_graph_copy", cfg("graph", K, c4, "copy", "batched")),
         ("c4_batched_direct_copy", cfg("direct", K, c4, "copy", "batched")),
