@@ -153,6 +153,12 @@ __device__ __forceinline__ void softmax_apply_1r(Row<V, VEC, EXACT> &r, float *o
   float M = -FLT_MAX;
   for (int k = 0; k < waves; ++k) M = fmaxf(M, slots[2 * k]);
   float S = 0.0f;
+  // Not unrolled: the unrolled loop's overlapping exps took the 8-float4 row
+  // kernel to 59 VGPRs; rolled it takes 54, and two waves of it (2 x 56
+  // allocated) fit on a SIMD beside the block-scaled contraction's two
+  // (2 x 200), so softmax rows run during that product. Same order of
+  // operations, same results.
+#pragma unroll 1
   for (int k = 0; k < waves; ++k) S += slots[2 * k + 1] * exp_nonpositive(slots[2 * k] - M);
   r.store_scaled(out, size, exp_nonpositive(m - M) / S, nullptr);
 }

@@ -435,26 +435,47 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_kernel(float *__restr
 // instructions), W codes 16 KB (16), the X scale words (1) and the W scales
 // (1). The W scales are staged 16 bytes a row, the scale words of four
 // consecutive steps (row-major [rows][cols / 32] bytes, so four steps of one
-// row are contiguous), into a three-slot ring: the DMA of step t carries part
-// (t + 5) % 4 (rows 64 part .. 64 part + 63) of the four-step group
-// (t + 5) / 4, so a group's four parts are issued by step 4 G - 2 and have
-// landed, by the one-step-ahead wait, before its first reader at step 4 G;
-// the slot a group refills was last read at step 4 G - 9. Needs
+// row are contiguous), into a three-slot ring: the DMA of step s carries part
+// (s + 3) % 4 (rows 64 part .. 64 part + 63) of the four-step group
+// (s + 3) / 4, so a group's four parts travel with the DMAs of steps
+// 4 G - 3 .. 4 G and have landed before its first reader, the W reads of
+// step 4 G; the slot a group refills was last read at step 4 G - 9. Needs
 // cols % 512 == 0 (whole four-step groups, 16-byte aligned scale rows).
 //
 // Waves: p = wave & 3 takes the 64 x 128 output sub-tile (wm = p & 1 of the
 // batch rows, wn = p >> 1 of the weight rows), 2 x 4 blocks of 32 x 32; wave
 // group g = wave >> 2 takes the k-slice [64 g, 64 g + 64) of every step, as in
-// scaled_gemm_kernel, whose ping-pong schedule, fragment placement and
-// swizzles this kernel keeps. Fragment reads per wave and step: 4 + 4 of 16
-// bytes, 2 + 4 scale words.
+// scaled_gemm_kernel, whose fragment placement and swizzles this kernel keeps.
+// Fragment reads per wave and step: 4 + 4 of 16 bytes, 2 + 4 scale words.
+//
+// Schedule: the ping-pong of scaled_gemm_kernel (the two wave groups half a
+// step apart, a barrier after each phase) with four LDS stages, so that the
+// X half of the fragment reads moves out of the memory phase. A wave's
+// memory phase of step t issues the DMA of step t + 3 into the stage step
+// t - 1 held, reads its W fragments and scale words of step t, waits for its
+// own DMA of step t + 2 and for its LDS reads, then the barrier; its MFMA
+// phase runs the step's 8 MFMAs while it reads its X fragments of step t + 1
+// into a second register set. Step t + 1 is complete in LDS by then: every
+// wave waited for its part of it one step earlier, before a barrier that
+// both groups have passed. A stage is refilled two phases after its last
+// reader's reads were waited for. Measured at 1024 x 16384 x 8192 against
+// the three-stage form with every fragment read in the memory phase, three
+// rounds on one box, results bit-identical: the product alone 108.1-108.3
+// against 115.8-119.9 µs, the C5 graph iteration 139.7-140.6 against
+// 148.2-151.0, direct 161.4-162.3 against 169.6. Reading the W half ahead
+// too (212 VGPRs) gave the same product time but slower iterations: two
+// waves of 212 VGPRs leave no room on a SIMD for the row kernels' waves
+// beside them (2 x 56), so rmsnorm and softmax no longer run during the
+// product. This form takes 195 (200 allocated), which leaves exactly that
+// room.
 constexpr int kWideBM = 128;
 constexpr int kWideBN = 256;
 constexpr int kWideXBytes = kWideBM * kBK;                  // 16 KB of X codes
 constexpr int kWideWBytes = kWideBN * 64;                   // 16 KB of E2M1 codes
 constexpr int kWideXS = kWideXBytes + kWideWBytes;          // X scale words (1 KB DMA, 512 B used)
 constexpr int kWideStage = kWideXS + 1024;
-constexpr int kWideRing = kStages * kWideStage;             // W scale ring: 3 x 256 rows x 16 B
+constexpr int kWideStages = 4;
+constexpr int kWideRing = kWideStages * kWideStage;         // W scale ring: 3 x 256 rows x 16 B
 constexpr int kWideRingSlot = kWideBN * 16;
 constexpr int kWideLds = kWideRing + 3 * kWideRingSlot > kExchange ? kWideRing + 3 * kWideRingSlot : kExchange;
 static_assert(kWideLds <= 160 * 1024, "the wide tile's stages fit the LDS");
@@ -558,17 +579,25 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_wide_kernel(float *__
   const int wr0 = wn * 128 + r;
   const int wa = kWideXBytes + wr0 * 64 + 16 * (blk ^ ((r >> 2) & 3));
   const int shift = 8 * blk;
-  u32x4 fa[2][2], fb[4];
-  unsigned sa[2], sb[4];
-  auto read = [&](int stage, int t) __attribute__((always_inline)) {
+  struct XFrag {
+    u32x4 fa[2][2];
+    unsigned sa[2];
+  };
+  XFrag fr0, fr1;
+  u32x4 fb[4];
+  unsigned sb[4];
+  auto read_x = [&](XFrag &f, int stage) __attribute__((always_inline)) {
     const unsigned char *base = lds + stage * kWideStage;
-    const unsigned char *ring = lds + kWideRing + ((t >> 2) % 3) * kWideRingSlot + (t & 3) * 4;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      fa[i][0] = *reinterpret_cast<const u32x4 *>(base + xa + 4096 * i + xc0);
-      fa[i][1] = *reinterpret_cast<const u32x4 *>(base + xa + 4096 * i + xc1);
-      sa[i] = *reinterpret_cast<const unsigned *>(base + kWideXS + (wm * 64 + 32 * i + r) * 4) >> shift;
+      f.fa[i][0] = *reinterpret_cast<const u32x4 *>(base + xa + 4096 * i + xc0);
+      f.fa[i][1] = *reinterpret_cast<const u32x4 *>(base + xa + 4096 * i + xc1);
+      f.sa[i] = *reinterpret_cast<const unsigned *>(base + kWideXS + (wm * 64 + 32 * i + r) * 4) >> shift;
     }
+  };
+  auto read_w = [&](int stage, int t) __attribute__((always_inline)) {
+    const unsigned char *base = lds + stage * kWideStage;
+    const unsigned char *ring = lds + kWideRing + ((t >> 2) % 3) * kWideRingSlot + (t & 3) * 4;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       fb[j] = *reinterpret_cast<const u32x4 *>(base + wa + 32 * 64 * j);
@@ -583,8 +612,9 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_wide_kernel(float *__
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  // Prologue: W scale parts 0-2 of group 0 (wave 5), then steps 0 and 1 with
-  // parts 3 and 4; the wait leaves only step 1's DMA outstanding.
+  // Prologue: W scale parts 0-2 of group 0 (wave 5), then steps 0-2 with
+  // parts 3-5; the wait leaves only step 2's DMA outstanding, and after the
+  // barrier every wave reads step 0's fragments.
   const int last = steps - 1;
   if (wave == 5) {
     scale_dma(0);
@@ -593,33 +623,52 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_wide_kernel(float *__
   }
   dma(0, 0, 3);
   dma(1, min(1, last), 4);
+  dma(2, min(2, last), 5);
   wait_dma_barrier();
+  read_x(fr0, 0);
   if (g == 1) barrier();
-  int cur = 0;
-  for (int t = 0; t < steps; ++t) {
-    dma(cur == 0 ? kStages - 1 : cur - 1, min(t + 2, last), t + 5);
-    read(cur, t);
+  // One step: the memory phase issues the DMA of step t + 3 into the stage
+  // step t - 1 held and reads step t's W fragments and scale words, waits for
+  // this wave's DMA of step t + 2 and for its LDS reads, then the barrier; the
+  // MFMA phase runs step t's 8 MFMAs on the X fragments in `use` while reading
+  // step t + 1's into `next`.
+  auto step = [&](int t, XFrag &use, XFrag &next) __attribute__((always_inline)) {
+    dma((t + 3) & 3, min(t + 3, last), t + 6);
+    read_w(t & 3, t);
     wait_dma_barrier();
     __builtin_amdgcn_s_setprio(1);
+    read_x(next, (t + 1) & 3);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       i32x8 a;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) a[c] = static_cast<int>(fa[i][0][c]), a[4 + c] = static_cast<int>(fa[i][1][c]);
+      for (int c = 0; c < 4; ++c) a[c] = static_cast<int>(use.fa[i][0][c]), a[4 + c] = static_cast<int>(use.fa[i][1][c]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         i32x8 b;
 #pragma unroll
         for (int c = 0; c < 4; ++c) b[c] = static_cast<int>(fb[j][c]), b[4 + c] = 0;
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc[i][j], kFmtE4M3, kFmtE2M1, 0,
-                                                                    static_cast<int>(sa[i]), 0,
+                                                                    static_cast<int>(use.sa[i]), 0,
                                                                     static_cast<int>(sb[j]));
       }
     }
+    // The 8 MFMAs with the 6 X reads (4 fragments, 2 scale words) between them.
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     __builtin_amdgcn_s_setprio(0);
     barrier();
-    cur = cur == kStages - 1 ? 0 : cur + 1;
+  };
+  int t = 0;
+  for (; t + 1 < steps; t += 2) {
+    step(t, fr0, fr1);
+    step(t + 1, fr1, fr0);
   }
+  if (t < steps) step(t, fr0, fr1);
   if (g == 0) barrier();
 
   // Partial sums of the two k-slices: group 1 stores, group 0 adds and writes.
