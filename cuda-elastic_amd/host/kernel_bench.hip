@@ -30,7 +30,10 @@
 // written), the form that leaves dirty lines behind. `read_cold` times the
 // read-only sweep kernel itself over W's bytes after the same flush: a plain
 // streaming read of that many bytes from HBM, the rate an isolated product of
-// that size can hope for.
+// that size can hope for. `rmsnorm_cold` and `softmax_cold` time the row
+// kernels after the same read-only flush, so their rows come from HBM; run
+// back to back (`rmsnorm`, `softmax`), a 64 MiB input stays in the MALL.
+// `copy_cold` is the plain copy of BATCH x SIZE floats after that flush.
 //
 // `vendor_f32` and `vendor_bf16` time the vendor library's GEMM of the same
 // contraction (hipBLASLt, out[b][r] = sum_k X[b][k] W[r][k] with fp32 or bf16
@@ -480,7 +483,8 @@ int main(int argc, char **argv) {
   }
   const size_t vec = static_cast<size_t>(B) * S, mat = static_cast<size_t>(R) * S;
   float *x = nullptr, *p = nullptr, *w = nullptr, *m = nullptr, *o1 = nullptr, *o2 = nullptr, *prod = nullptr;
-  const bool needs_matrix = op != "rmsnorm" && op != "softmax" && op != "copy";
+  const bool needs_matrix = op != "rmsnorm" && op != "softmax" && op != "copy" && op != "rmsnorm_cold" &&
+                            op != "softmax_cold" && op != "copy_cold";
   CHECK(hipMalloc(&x, vec * 4));
   CHECK(hipMalloc(&p, vec * 4));
   CHECK(hipMalloc(&w, static_cast<size_t>(S) * 4));
@@ -642,7 +646,8 @@ int main(int argc, char **argv) {
   hipEvent_t t0, t1;
   CHECK(hipEventCreate(&t0));
   CHECK(hipEventCreate(&t1));
-  if (op == "gemv_cold" || op == "gemv_cold_copy" || op == "read_cold") {
+  if (op == "gemv_cold" || op == "gemv_cold_copy" || op == "read_cold" || op == "rmsnorm_cold" ||
+      op == "softmax_cold" || op == "copy_cold") {
     constexpr size_t kFlush = size_t(1) << 30;  // 1 GiB: four times the MALL
     float4 *fa = nullptr, *fb = nullptr;
     float *sink = nullptr;
@@ -669,6 +674,13 @@ int main(int argc, char **argv) {
       if (op == "read_cold")
         hipLaunchKernelGGL(sweep_kernel, dim3(4096), dim3(256), 0, s, reinterpret_cast<const float4 *>(m), mat / 4,
                            1.0e30f, sink);
+      else if (op == "rmsnorm_cold")
+        L2C(l2c_rmsnorm(o1, x, w, S, B, 1.0e-5f, s));
+      else if (op == "softmax_cold")
+        L2C(l2c_softmax(o2, p, S, B, s));
+      else if (op == "copy_cold")
+        hipLaunchKernelGGL(copy_kernel, dim3(4096), dim3(256), 0, s, reinterpret_cast<float4 *>(o1),
+                           reinterpret_cast<const float4 *>(x), vec / 4);
       else
         L2C(l2c_matvec(prod, x, m, S, R, L2C_MATVEC_COALESCED, s));
       CHECK(hipGetLastError());
@@ -680,7 +692,10 @@ int main(int argc, char **argv) {
       if (i >= 3) total_ms += ms, flush_ms += fms;  // three untimed rounds first
     }
     const double us = 1000.0 * total_ms / iters;
-    const double bytes = op == "read_cold" ? mat * 4.0 : mat * 4.0 + (S + static_cast<double>(R)) * 4;
+    const double bytes = op == "read_cold"      ? mat * 4.0
+                         : op == "rmsnorm_cold" ? 2.0 * vec * 4 + S * 4.0
+                         : op == "softmax_cold" || op == "copy_cold" ? 2.0 * vec * 4
+                                                : mat * 4.0 + (S + static_cast<double>(R)) * 4;
     std::printf("op=%s batch=%d size=%d rows=%d iters=%d avg_us=%.3f bytes=%.0f gbps=%.1f flush=%s flush_us=%.1f\n",
                 op.c_str(), B, S, R, iters, us, bytes, bytes / (us * 1e3), copy_flush ? "copy_512MiB" : "read_1GiB",
                 1000.0 * flush_ms / iters);

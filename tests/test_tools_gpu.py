@@ -17,7 +17,7 @@ BENCH = os.path.join(PKG, "bin", "l2c_kernel_bench")
 SHAPE = (256, 1024, 512)  # batch, size (k), rows: every op's divisibility holds
 OPS = ["rmsnorm", "softmax", "gemv", "naive", "fused", "matmul", "mxfp4", "fp8", "mxfp4s", "mxfp4s_narrow", "fp8s",
        "cvt_mxfp8", "bf16", "mxfp6", "cvt_bf16", "cvt_mxfp6", "cvt_nvfp4", "copy", "gemv_cold", "gemv_cold_copy",
-       "read_cold", "vendor_f32", "vendor_bf16"]
+       "read_cold", "rmsnorm_cold", "softmax_cold", "copy_cold", "vendor_f32", "vendor_bf16"]
 
 
 def run(*args, timeout=180):
@@ -32,7 +32,7 @@ def test_op_runs(torch_gpu, op):
     line = r.stdout.strip().splitlines()[-1]
     assert line.startswith(f"op={op} batch={SHAPE[0]} size={SHAPE[1]} rows={SHAPE[2]} "), line
     assert float(re.search(r"avg_us=([0-9.]+)", line).group(1)) > 0.0
-    if op in ("gemv_cold", "gemv_cold_copy", "read_cold"):
+    if op.endswith("_cold") or op == "gemv_cold_copy":
         assert ("flush=copy_512MiB" if op == "gemv_cold_copy" else "flush=read_1GiB") in line
 
 
