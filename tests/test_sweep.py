@@ -126,3 +126,41 @@ def test_launch_trace_summary_on_a_synthetic_trace(tmp_path):
     assert s["steady"]["kernels"] == 4 and s["steady"]["gap_median_us"] == 17.0
     assert s["steady"]["busy_frac"] == round(12.0 / 63.0, 3)
     assert s["call_end_to_kernel_start_us"]["hipGraphLaunch"]["median"] == 5.0
+
+
+def test_overlap_summary_on_a_synthetic_trace(tmp_path):
+    """l2c.overlap on a trace whose figures are known: 8 iterations 130 us
+    apart, a 100 us product, rmsnorm inside it (+5 .. +45 us) and softmax
+    after it (+100 .. +125 us, so it belongs to the gap before the next
+    product)."""
+    from l2c import overlap
+
+    kernels = []
+    for i in range(8):
+        p0 = 1_000_000 + i * 130_000
+        kernels.append({"Kernel_Name": "scaled_gemm_wide_kernel(float*)", "Start_Timestamp": str(p0),
+                        "End_Timestamp": str(p0 + 100_000)})
+        kernels.append({"Kernel_Name": "rmsnorm_kernel<8>", "Start_Timestamp": str(p0 + 5_000),
+                        "End_Timestamp": str(p0 + 45_000)})
+        kernels.append({"Kernel_Name": "softmax_kernel<8>", "Start_Timestamp": str(p0 + 100_000),
+                        "End_Timestamp": str(p0 + 125_000)})
+    d = tmp_path / "trace" / "host"
+    d.mkdir(parents=True)
+    with open(d / "t_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(kernels[0]))
+        w.writeheader()
+        w.writerows(kernels)
+    # The harness also times the product alone: 4 launches back to back, no rows.
+    p0 = 1_000_000 + 8 * 130_000 + 50_000
+    for i in range(4):
+        kernels.append({"Kernel_Name": "scaled_gemm_wide_kernel(float*)", "Start_Timestamp": str(p0 + i * 100_000),
+                        "End_Timestamp": str(p0 + (i + 1) * 100_000)})
+    with open(d / "t_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(kernels[0]))
+        w.writeheader()
+        w.writerows(kernels)
+    s = overlap.summarize_dir(str(tmp_path / "trace"), "scaled_gemm_wide", ["rmsnorm", "softmax"])
+    assert s["launches"] == 12 and s["iterations"] == 8 and s["steady_iterations"] == 4
+    assert s["product_us"] == 100.0 and s["gap_us"] == 30.0 and s["period_us"] == 130.0
+    assert s["rows"]["rmsnorm"] == {"n": 4, "start_us": 5.0, "end_us": 45.0, "inside_product": 1.0}
+    assert s["rows"]["softmax"] == {"n": 4, "start_us": -30.0, "end_us": -5.0, "inside_product": 0.0}
