@@ -200,7 +200,8 @@ def test_launch_shape_names_the_tile_the_product_runs(torch_gpu, l2c):
     assert l2c.launch_shape(l2c.OP_MATMUL_QS, 1024, 16384, 8192, l2c.Q_MXFP4)[2] == 1
 
 
-@pytest.mark.parametrize("batch,cols,rows", [(130, 1536, 600), (1024, 16384, 1024)])
+@pytest.mark.parametrize("batch,cols,rows", [(1, 512, 1), (257, 512, 257), (130, 1536, 600), (64, 2048, 4096),
+                                             (1024, 16384, 1024)])
 def test_wide_and_narrow_mxfp4_tiles_agree_bit_for_bit(torch_gpu, l2c, orc, batch, cols, rows):
     """MXFP4 products with cols % 512 == 0 run on the 128 x 256 tile when the
     scale array is 16-byte aligned and on the 256 x 128 tile otherwise; every
