@@ -51,8 +51,9 @@
 //    stages there, one step for the DMA, measured 213 µs). The 128 x 256
 //    tile gives the same results bit for bit with 32 KB stages: alone within
 //    1% (209 against 207 µs on the harness's weights), the graph iteration
-//    252 against 281 µs. MXFP4 on it measured 226 against 216 µs and keeps
-//    256 x 128. Issuing the fragment reads ahead of the DMA measured 1-1.3%
+//    252 against 281 µs. MXFP4 on it measured 226 against 216 µs (213 against
+//    197.5 µs with the present schedule, three rounds on one box, bit-identical)
+//    and keeps 256 x 128. Issuing the fragment reads ahead of the DMA measured 1-1.3%
 //    faster than the DMA first (fp8 201.4-202.9 against 203.3-204.7 µs,
 //    MXFP4 203.0-203.5 against 205.6-206.0 µs).
 //  * Every access is in bounds by construction: rows past the operand are
