@@ -226,3 +226,37 @@ def test_wide_and_narrow_mxfp4_tiles_agree_bit_for_bit(torch_gpu, l2c, orc, batc
     w, n = wide.cpu().numpy(), narrow.cpu().numpy()
     assert np.isfinite(w).all()
     np.testing.assert_array_equal(w.view(np.uint32), n.view(np.uint32))
+
+
+def test_wide_and_narrow_mxfp4_tiles_agree_on_random_shapes(torch_gpu, l2c):
+    """Seeded random shapes (ragged batch and rows, K from 512 to 4096) through
+    both MXFP4 tiles: bit-identical outputs, every one finite. Operands are
+    random device data quantized by the library, so no oracle is involved; the
+    oracle comparison of the narrow tile is in the tests above."""
+    torch = torch_gpu
+    rng = np.random.default_rng(2026)
+    for case in range(12):
+        batch = int(rng.integers(1, 700))
+        rows = int(rng.integers(1, 1500))
+        cols = 512 * int(rng.integers(1, 9))
+        print(f"case random wide/narrow mxfp4s #{case} {batch}x{cols}x{rows}", flush=True)
+        g = torch.Generator(device="cuda").manual_seed(case)
+        x = torch.randn(batch * cols, device="cuda", generator=g) * float(rng.uniform(0.1, 4.0))
+        w = torch.randn(rows * cols, device="cuda", generator=g) * float(rng.uniform(1e-3, 1.0))
+        codes = torch.empty(rows * cols // 2, dtype=torch.uint8, device="cuda")
+        scales = torch.empty(rows * cols // 32, dtype=torch.uint8, device="cuda")
+        l2c.quantize_mxfp4(codes, scales, w, rows, cols)
+        xbf = torch.empty(batch * cols, dtype=torch.int16, device="cuda")
+        l2c.to_bf16(xbf, x, batch * cols)
+        ws = torch.empty(l2c.mxfp8_workspace_bytes(batch, cols), dtype=torch.uint8, device="cuda")
+        wide = torch.full((batch * rows,), float("nan"), dtype=torch.float32, device="cuda")
+        narrow = torch.full((batch * rows,), float("nan"), dtype=torch.float32, device="cuda")
+        holder = torch.zeros(scales.numel() + 16, dtype=torch.uint8, device="cuda")
+        shifted = holder[4:4 + scales.numel()]
+        shifted.copy_(scales)
+        l2c.matmul_qs(wide, xbf, codes, scales, 0, batch, cols, rows, ws)
+        l2c.matmul_qs(narrow, xbf, codes, shifted, 0, batch, cols, rows, ws)
+        torch.cuda.synchronize()
+        wn, nn = wide.cpu().numpy(), narrow.cpu().numpy()
+        assert np.isfinite(wn).all(), case
+        np.testing.assert_array_equal(wn.view(np.uint32), nn.view(np.uint32))
