@@ -34,6 +34,9 @@
 // kernels after the same read-only flush, so their rows come from HBM; run
 // back to back (`rmsnorm`, `softmax`), a 64 MiB input stays in the MALL.
 // `copy_cold` is the plain copy of BATCH x SIZE floats after that flush.
+// `read` is the flush's read-only sweep over BATCH x SIZE floats, back to
+// back: with up to ~256 MB the data stays in the MALL, so it is the rate the
+// MALL delivers to the CUs (the ceiling of the back-to-back C2 product).
 //
 // `vendor_f32` and `vendor_bf16` time the vendor library's GEMM of the same
 // contraction (hipBLASLt, out[b][r] = sum_k X[b][k] W[r][k] with fp32 or bf16
@@ -484,7 +487,7 @@ int main(int argc, char **argv) {
   const size_t vec = static_cast<size_t>(B) * S, mat = static_cast<size_t>(R) * S;
   float *x = nullptr, *p = nullptr, *w = nullptr, *m = nullptr, *o1 = nullptr, *o2 = nullptr, *prod = nullptr;
   const bool needs_matrix = op != "rmsnorm" && op != "softmax" && op != "copy" && op != "rmsnorm_cold" &&
-                            op != "softmax_cold" && op != "copy_cold";
+                            op != "softmax_cold" && op != "copy_cold" && op != "read";
   CHECK(hipMalloc(&x, vec * 4));
   CHECK(hipMalloc(&p, vec * 4));
   CHECK(hipMalloc(&w, static_cast<size_t>(S) * 4));
@@ -566,6 +569,8 @@ int main(int argc, char **argv) {
 
   hipStream_t s;
   CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  float *read_sink = nullptr;
+  if (op == "read") CHECK(hipMalloc(&read_sink, 4));
   VendorGemm vg;
   if (vendor) {
     const bool bf = op == "vendor_bf16";
@@ -633,6 +638,11 @@ int main(int argc, char **argv) {
       vg.run(prod, wb, xb, s);
       bytes = (vec + static_cast<double>(mat)) * 2 + static_cast<double>(B) * R * 4;
       flops = 2.0 * B * static_cast<double>(mat);
+    } else if (op == "read") {
+      hipLaunchKernelGGL(sweep_kernel, dim3(4096), dim3(256), 0, s, reinterpret_cast<const float4 *>(x), vec / 4,
+                         1.0e30f, read_sink);
+      CHECK(hipGetLastError());
+      bytes = vec * 4.0;
     } else if (op == "copy") {
       hipLaunchKernelGGL(copy_kernel, dim3(4096), dim3(256), 0, s, reinterpret_cast<float4 *>(o1),
                          reinterpret_cast<const float4 *>(x), vec / 4);
