@@ -427,13 +427,19 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_kernel(float *__restr
 
 // ---------------------------------------------------------------------------
 // The MXFP4 contraction on wide tiles: 128 (batch) x 256 (rows) x 128 (k per
-// step). The staging of both operands goes through the same L2 -> LDS DMA
-// return path, and the block-scaled kernels are bound by it: their time tracks
-// the number of LDS-DMA instructions (about 35 return-path cycles each per CU,
-// `TD_TD_BUSY` 0.86 of the cycles on the 256 x 128 tile). Per 64 MFMAs this
-// tile issues 34 DMA instructions against 43: X codes 16 KB (16 one-KB
-// instructions), W codes 16 KB (16), the X scale words (1) and the W scales
-// (1). The W scales are staged 16 bytes a row, the scale words of four
+// step). Both operands are staged by LDS DMA from L2, and the L2 serves a
+// request per row segment whatever its length up to a 128-byte line, so the
+// staging time tracks the number of row segments rather than the bytes. X
+// codes are 128 bytes a row and step (one line); the E2M1 W codes are only 64,
+// so W is staged two steps at a time: 256 rows x 128 bytes (steps 2 p and
+// 2 p + 1, 32 one-KB instructions, 4 a wave) into one of two pair slots every
+// other step. Per two steps that is 256 + 256 row segments against 256 + 512
+// with W staged a step at a time, at the same instruction count; a
+// staging-only copy of the two patterns (`l2c_kernel_bench stage_wpair` and
+// `stage_wstep`) measured 42.6 against 58.6 µs at 1024 x 16384 x 8192, the
+// kernel 106.9 against 108.0 µs (1%; the C5 graph iteration 136.4-137.8
+// against 138.4-139.8), results bit-identical. The W scales are staged 16
+// bytes a row, the scale words of four
 // consecutive steps (row-major [rows][cols / 32] bytes, so four steps of one
 // row are contiguous), into a three-slot ring: the DMA of step s carries part
 // (s + 3) % 4 (rows 64 part .. 64 part + 63) of the four-step group
@@ -449,10 +455,11 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_kernel(float *__restr
 // Fragment reads per wave and step: 4 + 4 of 16 bytes, 2 + 4 scale words.
 //
 // Schedule: the ping-pong of scaled_gemm_kernel (the two wave groups half a
-// step apart, a barrier after each phase) with four LDS stages, so that the
+// step apart, a barrier after each phase) with four X stages, so that the
 // X half of the fragment reads moves out of the memory phase. A wave's
-// memory phase of step t issues the DMA of step t + 3 into the stage step
-// t - 1 held, reads its W fragments and scale words of step t, waits for its
+// memory phase of step t issues the X DMA of step t + 3 into the stage step
+// t - 1 held (and on even steps first the W pair of steps t + 2, t + 3),
+// reads its W fragments and scale words of step t, waits for its
 // own DMA of step t + 2 and for its LDS reads, then the barrier; its MFMA
 // phase runs the step's 8 MFMAs while it reads its X fragments of step t + 1
 // into a second register set. Step t + 1 is complete in LDS by then: every
@@ -466,16 +473,17 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_kernel(float *__restr
 // too (212 VGPRs) gave the same product time but slower iterations: two
 // waves of 212 VGPRs leave no room on a SIMD for the row kernels' waves
 // beside them (2 x 56), so rmsnorm and softmax no longer run during the
-// product. This form takes 195 (200 allocated), which leaves exactly that
+// product. This form takes 198 (200 allocated), which leaves exactly that
 // room.
 constexpr int kWideBM = 128;
 constexpr int kWideBN = 256;
 constexpr int kWideXBytes = kWideBM * kBK;                  // 16 KB of X codes
-constexpr int kWideWBytes = kWideBN * 64;                   // 16 KB of E2M1 codes
-constexpr int kWideXS = kWideXBytes + kWideWBytes;          // X scale words (1 KB DMA, 512 B used)
-constexpr int kWideStage = kWideXS + 1024;
+constexpr int kWideXS = kWideXBytes;                        // X scale words (1 KB DMA, 512 B used)
+constexpr int kWideStage = kWideXS + 1024;                  // one step's X codes and scale words
 constexpr int kWideStages = 4;
-constexpr int kWideRing = kWideStages * kWideStage;         // W scale ring: 3 x 256 rows x 16 B
+constexpr int kWidePairs = kWideStages * kWideStage;        // 2 W slots: 256 rows x 128 B (two steps)
+constexpr int kWidePair = kWideBN * 128;
+constexpr int kWideRing = kWidePairs + 2 * kWidePair;       // W scale ring: 3 x 256 rows x 16 B
 constexpr int kWideRingSlot = kWideBN * 16;
 constexpr int kWideLds = kWideRing + 3 * kWideRingSlot > kExchange ? kWideRing + 3 * kWideRingSlot : kExchange;
 static_assert(kWideLds <= 160 * 1024, "the wide tile's stages fit the LDS");
@@ -513,19 +521,24 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_wide_kernel(float *__
 
   // Per-lane DMA sources. X: instruction 8 k + wave (k < 2) fills rows
   // 8 (8 k + wave) + lane / 8, slot lane % 8 with chunk slot ^ xswizzle(row).
-  // W: instruction 8 k + wave fills rows 16 (8 k + wave) + lane / 4, slot
-  // lane % 4 with chunk slot ^ ((row >> 2) & 3). X scales (wave 4): rows
-  // 4 lane .. 4 lane + 3 (lanes past the tile read the last rows again into
-  // the unused half). W scales (wave 5): row 64 part + lane.
-  int xsrc[2], wsrc[2];
+  // W pairs (128 bytes a row: step 2 p in chunks 0-3, step 2 p + 1 in 4-7):
+  // instruction 8 k + wave (k < 4) fills rows 8 (8 k + wave) + lane / 8 the
+  // same way. X scales (wave 4): rows 4 lane .. 4 lane + 3 (lanes past the
+  // tile read the last rows again into the unused half). W scales (wave 5):
+  // row 64 part + lane.
+  int xsrc[2], wsrc[4];
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int xrow = 8 * (8 * k + wave) + lane / 8;
     xsrc[k] = min(xrow, mrows - 1) * K + 16 * ((lane % 8) ^ xswizzle(xrow));
-    const int wrow = 16 * (8 * k + wave) + lane / 4;
-    wsrc[k] = min(wrow, nrows - 1) * wrb + 16 * ((lane % 4) ^ ((wrow >> 2) & 3));
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int wrow = 8 * (8 * k + wave) + lane / 8;
+    wsrc[k] = min(wrow, nrows - 1) * wrb + 16 * ((lane % 8) ^ xswizzle(wrow));
   }
   const int xssrc = min(16 * lane, (Mp - m0) * 4 - 16);
+  const int last_pair = steps / 2 - 1;
 
   // The W scale part u (group u / 4, rows 64 (u % 4) + lane) into its ring
   // slot; groups past the last re-read the last group into a slot no step
@@ -537,29 +550,43 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_wide_kernel(float *__
         rws, (lds_ptr *)(lds + kWideRing + ((u >> 2) % 3) * kWideRingSlot + 64 * part * 16), 16, row * srb,
         16 * group, 0, 0);
   };
+  // W pair p (steps 2 p and 2 p + 1) into slot p % 2; pairs past the last
+  // re-read the last one into the slot no step reads any more.
+  auto pair_dma = [&](int p) __attribute__((always_inline)) {
+    unsigned char *base = lds + kWidePairs + (p & 1) * kWidePair;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + (8 * k + wave) * 1024), 16, wsrc[k],
+                                               128 * min(p, last_pair), 0, 0);
+  };
   auto dma = [&](int stage, int t, int u) __attribute__((always_inline)) {
     unsigned char *base = lds + stage * kWideStage;
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
+    for (int k = 0; k < 2; ++k)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr *)(base + (8 * k + wave) * 1024), 16, xsrc[k], kBK * t,
                                                0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr *)(base + kWideXBytes + (8 * k + wave) * 1024), 16,
-                                               wsrc[k], 64 * t, 0, 0);
-    }
     if (wave == 4)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rxs, (lds_ptr *)(base + kWideXS), 16, xssrc, Mp * 4 * t + m0 * 4, 0,
                                                0);
     if (wave == 5) scale_dma(u);
   };
-  // This wave's DMA of the older of two outstanding steps has landed (4
-  // instructions a step, 5 on waves 4 and 5) and its LDS reads are done;
-  // then the workgroup barrier.
-  auto wait_dma_barrier = [&]() __attribute__((always_inline)) {
+  // This wave's DMA of step t + 2 has landed and its LDS reads are done; then
+  // the workgroup barrier. Outstanding after the wait: the X DMA of step t + 3
+  // (2 instructions, 3 on waves 4 and 5) and, on even steps, the W pair
+  // issued before it (4).
+  auto wait_dma_barrier = [&](bool pair_issued) __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
-    if (wave == 4 || wave == 5)
-      asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (pair_issued) {
+      if (wave == 4 || wave == 5)
+        asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+      if (wave == 4 || wave == 5)
+        asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
   auto barrier = [&]() __attribute__((always_inline)) {
@@ -570,14 +597,16 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_wide_kernel(float *__
 
   // Fragments of lane (r, h) for the instruction over the step's blocks 2 g
   // and 2 g + 1: X rows wm * 64 + 32 i + r, chunks 4 g + h and 4 g + 2 + h; W
-  // rows wn * 128 + 32 j + r, chunk 2 g + h; scale byte 2 g + h of each row's
-  // step word (X from the stage, W from the ring slot of the step's group).
+  // rows wn * 128 + 32 j + r, chunk 2 g + h of the step's half of the pair
+  // row; scale byte 2 g + h of each row's step word (X from the stage, W from
+  // the ring slot of the step's group). The swizzles of rows + 32 j equal r's.
   const int blk = 2 * g + h;
   const int xsw = xswizzle(r);
   const int xa = (wm * 64 + r) * 128;
   const int xc0 = 16 * ((4 * g + h) ^ xsw), xc1 = 16 * ((4 * g + 2 + h) ^ xsw);
   const int wr0 = wn * 128 + r;
-  const int wa = kWideXBytes + wr0 * 64 + 16 * (blk ^ ((r >> 2) & 3));
+  const int wa0 = kWidePairs + wr0 * 128 + 16 * (blk ^ xsw);        // even steps
+  const int wa1 = kWidePairs + wr0 * 128 + 16 * ((4 + blk) ^ xsw);  // odd steps
   const int shift = 8 * blk;
   struct XFrag {
     u32x4 fa[2][2];
@@ -595,12 +624,12 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_wide_kernel(float *__
       f.sa[i] = *reinterpret_cast<const unsigned *>(base + kWideXS + (wm * 64 + 32 * i + r) * 4) >> shift;
     }
   };
-  auto read_w = [&](int stage, int t) __attribute__((always_inline)) {
-    const unsigned char *base = lds + stage * kWideStage;
+  auto read_w = [&](int t) __attribute__((always_inline)) {
+    const unsigned char *base = lds + ((t >> 1) & 1) * kWidePair + ((t & 1) ? wa1 : wa0);
     const unsigned char *ring = lds + kWideRing + ((t >> 2) % 3) * kWideRingSlot + (t & 3) * 4;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      fb[j] = *reinterpret_cast<const u32x4 *>(base + wa + 32 * 64 * j);
+      fb[j] = *reinterpret_cast<const u32x4 *>(base + 32 * 128 * j);
       sb[j] = *reinterpret_cast<const unsigned *>(ring + (wr0 + 32 * j) * 16) >> shift;
     }
   };
@@ -612,30 +641,36 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_wide_kernel(float *__
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  // Prologue: W scale parts 0-2 of group 0 (wave 5), then steps 0-2 with
-  // parts 3-5; the wait leaves only step 2's DMA outstanding, and after the
-  // barrier every wave reads step 0's fragments.
+  // Prologue: W scale parts 0-2 of group 0 (wave 5), W pair 0, then X steps
+  // 0-2 with parts 3-5; the wait leaves only step 2's X outstanding, and after
+  // the barrier every wave reads step 0's fragments.
   const int last = steps - 1;
   if (wave == 5) {
     scale_dma(0);
     scale_dma(1);
     scale_dma(2);
   }
+  pair_dma(0);
   dma(0, 0, 3);
   dma(1, min(1, last), 4);
   dma(2, min(2, last), 5);
-  wait_dma_barrier();
+  wait_dma_barrier(false);
   read_x(fr0, 0);
   if (g == 1) barrier();
-  // One step: the memory phase issues the DMA of step t + 3 into the stage
-  // step t - 1 held and reads step t's W fragments and scale words, waits for
-  // this wave's DMA of step t + 2 and for its LDS reads, then the barrier; the
-  // MFMA phase runs step t's 8 MFMAs on the X fragments in `use` while reading
-  // step t + 1's into `next`.
-  auto step = [&](int t, XFrag &use, XFrag &next) __attribute__((always_inline)) {
+  // One step: the memory phase issues (on even steps) the W pair of steps
+  // t + 2 and t + 3 into the slot the pair of steps t - 2 and t - 1 held and
+  // the X DMA of step t + 3 into the stage step t - 1 held, reads step t's W
+  // fragments and scale words, waits for this wave's DMA of step t + 2 (and so
+  // for the pair of steps t + 1, t + 2 on odd steps) and for its LDS reads,
+  // then the barrier; the MFMA phase runs step t's 8 MFMAs on the X fragments
+  // in `use` while reading step t + 1's into `next`. A pair is issued one step
+  // before its wait, as X is: the pair of steps 2 p, 2 p + 1 at step 2 p - 2,
+  // waited at step 2 p - 1; its slot was last read at step 2 p - 3.
+  auto step = [&](int t, bool even, XFrag &use, XFrag &next) __attribute__((always_inline)) {
+    if (even) pair_dma((t >> 1) + 1);
     dma((t + 3) & 3, min(t + 3, last), t + 6);
-    read_w(t & 3, t);
-    wait_dma_barrier();
+    read_w(t);
+    wait_dma_barrier(even);
     __builtin_amdgcn_s_setprio(1);
     read_x(next, (t + 1) & 3);
 #pragma unroll
@@ -663,12 +698,11 @@ __global__ __launch_bounds__(kThreads, 1) void scaled_gemm_wide_kernel(float *__
     __builtin_amdgcn_s_setprio(0);
     barrier();
   };
-  int t = 0;
-  for (; t + 1 < steps; t += 2) {
-    step(t, fr0, fr1);
-    step(t + 1, fr1, fr0);
+  // steps is a multiple of 4 (cols % 512 == 0), so every pair is whole.
+  for (int t = 0; t < steps; t += 2) {
+    step(t, true, fr0, fr1);
+    step(t + 1, false, fr1, fr0);
   }
-  if (t < steps) step(t, fr0, fr1);
   if (g == 0) barrier();
 
   // Partial sums of the two k-slices: group 1 stores, group 0 adds and writes.
