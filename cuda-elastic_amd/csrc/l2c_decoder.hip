@@ -63,19 +63,29 @@ __device__ __forceinline__ float group_max(float v, float *slots) {
   return m;
 }
 
+// The workgroup's maximum of |normalized| (NaNs ignored, as fmaxf does) into
+// the word at `absmax` as float bits: non-negative floats order as their bit
+// patterns, so an unsigned atomic maximum is the float maximum, exactly and
+// in any order.
+__device__ __forceinline__ void publish_absmax(float m, float *mslots, unsigned *absmax) {
+  m = group_max(m, mslots);
+  if (threadIdx.x == 0) atomicMax(absmax, __float_as_uint(m));
+}
+
 // llama2.c rmsnorm of the embedding row of each sequence's current token
 // (decoder.cu:45-77): ss = sum x^2; ss /= width; ss += 1e-5f;
 // scale = 1 / sqrtf(ss); o_j = w_j * (scale * x_j). An out-of-range token
 // (a corrupted state, or the poisoned token buffer) gives a NaN row, so the
 // check fails instead of reading outside the embedding.
-template <bool VEC>
+template <bool VEC, bool AMAX>
 __global__ __launch_bounds__(kThreads) void decoder_rmsnorm_kernel(float *normalized,
                                                                    const int *tokens,
                                                                    const float *embedding,
                                                                    const float *weight, int width,
-                                                                   int vocab) {
+                                                                   int vocab, unsigned *absmax) {
 #pragma clang fp contract(off)  // separate multiply and add, as the contract's builds
   __shared__ float slots[kWaves];
+  __shared__ float mslots[kWaves];
   const int sequence = blockIdx.x;
   const int token = tokens[sequence];
   float *o = normalized + static_cast<size_t>(sequence) * width;
@@ -102,29 +112,38 @@ __global__ __launch_bounds__(kThreads) void decoder_rmsnorm_kernel(float *normal
   ss /= static_cast<float>(width);
   ss += 1e-5f;
   const float scale = 1.0f / sqrtf(ss);
+  float m = 0.0f;
   if constexpr (VEC) {
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     const float4 *w4 = reinterpret_cast<const float4 *>(weight);
     float4 *o4 = reinterpret_cast<float4 *>(o);
     for (int c = t; c < width / 4; c += kThreads) {
       const float4 v = x4[c], g = w4[c];
-      o4[c] = make_float4(g.x * (scale * v.x), g.y * (scale * v.y), g.z * (scale * v.z),
-                          g.w * (scale * v.w));
+      const float4 y = make_float4(g.x * (scale * v.x), g.y * (scale * v.y), g.z * (scale * v.z),
+                                   g.w * (scale * v.w));
+      o4[c] = y;
+      if constexpr (AMAX) m = fmaxf(m, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
     }
   } else {
-    for (int j = t; j < width; j += kThreads) o[j] = weight[j] * (scale * x[j]);
+    for (int j = t; j < width; j += kThreads) {
+      const float y = weight[j] * (scale * x[j]);
+      o[j] = y;
+      if constexpr (AMAX) m = fmaxf(m, fabsf(y));
+    }
   }
+  if constexpr (AMAX) publish_absmax(m, mslots, absmax);
 }
 
 // Register-resident rmsnorm: lane t holds float4 chunks t + 256 c (VEC) or
 // values t + 256 i of the row, c < CHUNKS (4 * CHUNKS values a lane).
-template <int CHUNKS, bool VEC>
+template <int CHUNKS, bool VEC, bool AMAX>
 __global__ __launch_bounds__(kThreads) void decoder_rmsnorm_regs_kernel(float *normalized, const int *tokens,
                                                                         const float *embedding,
                                                                         const float *weight, int width,
-                                                                        int vocab) {
+                                                                        int vocab, unsigned *absmax) {
 #pragma clang fp contract(off)
   __shared__ float slots[kWaves];
+  __shared__ float mslots[kWaves];
   const int sequence = blockIdx.x;
   const int token = tokens[sequence];
   float *o = normalized + static_cast<size_t>(sequence) * width;
@@ -157,6 +176,7 @@ __global__ __launch_bounds__(kThreads) void decoder_rmsnorm_regs_kernel(float *n
   ss /= static_cast<float>(width);
   ss += 1e-5f;
   const float scale = 1.0f / sqrtf(ss);
+  float m = 0.0f;
   if constexpr (VEC) {
     const float4 *w4 = reinterpret_cast<const float4 *>(weight);
     float4 *o4 = reinterpret_cast<float4 *>(o);
@@ -165,17 +185,24 @@ __global__ __launch_bounds__(kThreads) void decoder_rmsnorm_regs_kernel(float *n
       const int i = t + c * kThreads;
       if (i < width / 4) {
         const float4 g = w4[i];
-        o4[i] = make_float4(g.x * (scale * v[4 * c]), g.y * (scale * v[4 * c + 1]), g.z * (scale * v[4 * c + 2]),
-                            g.w * (scale * v[4 * c + 3]));
+        const float4 y = make_float4(g.x * (scale * v[4 * c]), g.y * (scale * v[4 * c + 1]),
+                                     g.z * (scale * v[4 * c + 2]), g.w * (scale * v[4 * c + 3]));
+        o4[i] = y;
+        if constexpr (AMAX) m = fmaxf(m, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
       }
     }
   } else {
 #pragma unroll
     for (int i = 0; i < 4 * CHUNKS; ++i) {
       const int j = t + i * kThreads;
-      if (j < width) o[j] = weight[j] * (scale * v[i]);
+      if (j < width) {
+        const float y = weight[j] * (scale * v[i]);
+        o[j] = y;
+        if constexpr (AMAX) m = fmaxf(m, fabsf(y));
+      }
     }
   }
+  if constexpr (AMAX) publish_absmax(m, mslots, absmax);
 }
 
 // The VEC register-resident rmsnorm over ROWS consecutive sequences per
@@ -194,9 +221,9 @@ __device__ __forceinline__ void rms_row_load(float4 (&dst)[CHUNKS], const float 
     dst[c] = ok && t + c * kThreads < n4 ? x4[t + c * kThreads] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
-template <int CHUNKS>
+template <int CHUNKS, bool AMAX>
 __device__ __forceinline__ void rms_row_store(float *o, const float4 (&v)[CHUNKS], const float4 (&g)[CHUNKS],
-                                              bool ok, float *slots, int width, int t) {
+                                              bool ok, float *slots, int width, int t, float &m) {
 #pragma clang fp contract(off)
   float ss = 0.0f;
 #pragma unroll
@@ -216,10 +243,13 @@ __device__ __forceinline__ void rms_row_store(float *o, const float4 (&v)[CHUNKS
 #pragma unroll
   for (int c = 0; c < CHUNKS; ++c) {
     const int i = t + c * kThreads;
-    if (i < n4)
-      o4[i] = ok ? make_float4(g[c].x * (scale * v[c].x), g[c].y * (scale * v[c].y), g[c].z * (scale * v[c].z),
-                               g[c].w * (scale * v[c].w))
-                 : make_float4(nan, nan, nan, nan);
+    if (i < n4) {
+      const float4 y = ok ? make_float4(g[c].x * (scale * v[c].x), g[c].y * (scale * v[c].y),
+                                        g[c].z * (scale * v[c].z), g[c].w * (scale * v[c].w))
+                          : make_float4(nan, nan, nan, nan);
+      o4[i] = y;
+      if constexpr (AMAX) m = fmaxf(m, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+    }
   }
 }
 
@@ -231,13 +261,15 @@ __device__ __forceinline__ void rms_row_store(float *o, const float4 (&v)[CHUNKS
 // still gives every CU two workgroups.
 constexpr int kRowsPipelineMinBatch = 512;
 
-template <int CHUNKS, int ROWS>
+template <int CHUNKS, int ROWS, bool AMAX>
 __global__ __launch_bounds__(kThreads) void decoder_rmsnorm_rows_kernel(float *normalized, const int *tokens,
                                                                         const float *embedding,
                                                                         const float *weight, int width,
-                                                                        int vocab, int batch) {
+                                                                        int vocab, int batch, unsigned *absmax) {
   static_assert(ROWS % 2 == 0, "rows alternate between two register sets");
   __shared__ float slots[2][kWaves];
+  __shared__ float mslots[kWaves];
+  float m = 0.0f;
   const int t = threadIdx.x;
   const int first = blockIdx.x * ROWS;
   float4 g[CHUNKS], a[CHUNKS], b[CHUNKS];
@@ -253,18 +285,19 @@ __global__ __launch_bounds__(kThreads) void decoder_rmsnorm_rows_kernel(float *n
     const bool has_b = first + r + 1 < batch;
     const int token_b = has_b ? tokens[first + r + 1] : -1;
     if (has_b) rms_row_load(b, embedding, token_b, vocab, width, t);
-    rms_row_store(normalized + static_cast<size_t>(first + r) * width, a, g, token_a >= 0 && token_a < vocab,
-                  slots[0], width, t);
+    rms_row_store<CHUNKS, AMAX>(normalized + static_cast<size_t>(first + r) * width, a, g,
+                                token_a >= 0 && token_a < vocab, slots[0], width, t, m);
     if (!has_b) break;  // uniform across the workgroup
     const bool has_a = r + 2 < ROWS && first + r + 2 < batch;
     if (has_a) {
       token_a = tokens[first + r + 2];
       rms_row_load(a, embedding, token_a, vocab, width, t);
     }
-    rms_row_store(normalized + static_cast<size_t>(first + r + 1) * width, b, g, token_b >= 0 && token_b < vocab,
-                  slots[1], width, t);
+    rms_row_store<CHUNKS, AMAX>(normalized + static_cast<size_t>(first + r + 1) * width, b, g,
+                                token_b >= 0 && token_b < vocab, slots[1], width, t, m);
     if (!has_a) break;
   }
+  if constexpr (AMAX) publish_absmax(m, mslots, absmax);
 }
 
 // (value, index) maximum over the workgroup with ties to the smaller index;
@@ -458,19 +491,21 @@ extern "C" int l2c_decoder_init_model(float *embedding, float *classifier, float
   return hipSuccess;
 }
 
+namespace {
+
 // The smallest register-resident instance whose lanes hold n values, or
 // null for rows longer than 16384 (streamed instead).
-using RmsFn = void (*)(float *, const int *, const float *, const float *, int, int);
+using RmsFn = void (*)(float *, const int *, const float *, const float *, int, int, unsigned *);
 using SoftFn = void (*)(float *, const float *, int *, int *, int, int, int);
 
-template <bool VEC>
+template <bool VEC, bool AMAX>
 RmsFn rmsnorm_regs(int n) {
   const int per_lane = (n + kThreads - 1) / kThreads;
-  if (per_lane <= 4) return decoder_rmsnorm_regs_kernel<1, VEC>;
-  if (per_lane <= 8) return decoder_rmsnorm_regs_kernel<2, VEC>;
-  if (per_lane <= 16) return decoder_rmsnorm_regs_kernel<4, VEC>;
-  if (per_lane <= 32) return decoder_rmsnorm_regs_kernel<8, VEC>;
-  if (per_lane <= 64) return decoder_rmsnorm_regs_kernel<16, VEC>;
+  if (per_lane <= 4) return decoder_rmsnorm_regs_kernel<1, VEC, AMAX>;
+  if (per_lane <= 8) return decoder_rmsnorm_regs_kernel<2, VEC, AMAX>;
+  if (per_lane <= 16) return decoder_rmsnorm_regs_kernel<4, VEC, AMAX>;
+  if (per_lane <= 32) return decoder_rmsnorm_regs_kernel<8, VEC, AMAX>;
+  if (per_lane <= 64) return decoder_rmsnorm_regs_kernel<16, VEC, AMAX>;
   return nullptr;
 }
 
@@ -485,29 +520,47 @@ SoftFn softmax_regs(int n) {
   return nullptr;
 }
 
+template <bool AMAX>
+int launch_decoder_rmsnorm(float *normalized, const int *tokens, const float *embedding, const float *weight,
+                           int width, int vocab, int batch, unsigned *absmax, hipStream_t stream) {
+  const bool vec = width % 4 == 0 && l2c_aligned16(normalized) && l2c_aligned16(embedding) &&
+                   l2c_aligned16(weight);
+  const int per_lane = (width + kThreads - 1) / kThreads;
+  if (vec && per_lane > 32 && per_lane <= 64 && batch >= kRowsPipelineMinBatch) {
+    hipLaunchKernelGGL((decoder_rmsnorm_rows_kernel<16, 2, AMAX>), dim3((batch + 1) / 2), dim3(kThreads), 0, stream,
+                       normalized, tokens, embedding, weight, width, vocab, batch, absmax);
+  } else if (const RmsFn regs = vec ? rmsnorm_regs<true, AMAX>(width) : rmsnorm_regs<false, AMAX>(width)) {
+    hipLaunchKernelGGL(regs, dim3(batch), dim3(kThreads), 0, stream, normalized, tokens, embedding, weight, width,
+                       vocab, absmax);
+  } else if (vec)
+    hipLaunchKernelGGL((decoder_rmsnorm_kernel<true, AMAX>), dim3(batch), dim3(kThreads), 0, stream,
+                       normalized, tokens, embedding, weight, width, vocab, absmax);
+  else
+    hipLaunchKernelGGL((decoder_rmsnorm_kernel<false, AMAX>), dim3(batch), dim3(kThreads), 0, stream,
+                       normalized, tokens, embedding, weight, width, vocab, absmax);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+}  // namespace
+
 extern "C" int l2c_decoder_rmsnorm(float *normalized, const int *tokens, const float *embedding,
                                    const float *weight, int width, int vocab, int batch,
                                    hipStream_t stream) {
   if (width <= 0 || vocab <= 0 || batch < 0) return hipErrorInvalidValue;
   if (batch == 0) return hipSuccess;
   if (!normalized || !tokens || !embedding || !weight) return hipErrorInvalidValue;
-  const bool vec = width % 4 == 0 && l2c_aligned16(normalized) && l2c_aligned16(embedding) &&
-                   l2c_aligned16(weight);
-  const int per_lane = (width + kThreads - 1) / kThreads;
-  if (vec && per_lane > 32 && per_lane <= 64 && batch >= kRowsPipelineMinBatch) {
-    hipLaunchKernelGGL((decoder_rmsnorm_rows_kernel<16, 2>), dim3((batch + 1) / 2), dim3(kThreads), 0, stream,
-                       normalized, tokens, embedding, weight, width, vocab, batch);
-  } else if (const RmsFn regs = vec ? rmsnorm_regs<true>(width) : rmsnorm_regs<false>(width)) {
-    hipLaunchKernelGGL(regs, dim3(batch), dim3(kThreads), 0, stream, normalized, tokens, embedding, weight, width,
-                       vocab);
-  } else if (vec)
-    hipLaunchKernelGGL(decoder_rmsnorm_kernel<true>, dim3(batch), dim3(kThreads), 0, stream,
-                       normalized, tokens, embedding, weight, width, vocab);
-  else
-    hipLaunchKernelGGL(decoder_rmsnorm_kernel<false>, dim3(batch), dim3(kThreads), 0, stream,
-                       normalized, tokens, embedding, weight, width, vocab);
-  L2C_LAUNCH_CHECK();
-  return hipSuccess;
+  return launch_decoder_rmsnorm<false>(normalized, tokens, embedding, weight, width, vocab, batch, nullptr, stream);
+}
+
+extern "C" int l2c_decoder_rmsnorm_absmax(float *normalized, const int *tokens, const float *embedding,
+                                          const float *weight, int width, int vocab, int batch,
+                                          unsigned *absmax_bits, hipStream_t stream) {
+  if (width <= 0 || vocab <= 0 || batch < 0 || !absmax_bits) return hipErrorInvalidValue;
+  if (batch == 0) return hipSuccess;
+  if (!normalized || !tokens || !embedding || !weight) return hipErrorInvalidValue;
+  return launch_decoder_rmsnorm<true>(normalized, tokens, embedding, weight, width, vocab, batch, absmax_bits,
+                                      stream);
 }
 
 extern "C" int l2c_decoder_softmax_argmax(float *probabilities, const float *logits, int *tokens,

@@ -127,6 +127,21 @@ __global__ __launch_bounds__(kThreads) void nvfp4_scales_kernel(float *__restric
   }
 }
 
+// The same scales from a tensor maximum already held as float bits in
+// `absmax` (l2c_decoder_rmsnorm_absmax's), which is then cleared for the
+// next maximum. One lane.
+__global__ void nvfp4_scales_absmax_kernel(float *__restrict__ tensor_scales, float *__restrict__ alpha,
+                                           const float *__restrict__ other_decode, unsigned *__restrict__ absmax) {
+#pragma clang fp contract(off)
+  const float m = __uint_as_float(*absmax);
+  const float s = l2c::nvfp4_encode_scale(m);
+  const float d = 1.0f / s;
+  tensor_scales[0] = s;
+  tensor_scales[1] = d;
+  if (alpha) *alpha = d * *other_decode;
+  *absmax = 0u;
+}
+
 // Scale code UE4M3((a / 6) s), codes E2M1((v s) / f), each step an FP32
 // operation in this order; a zero scale code zeroes the block. Optionally also
 // the exact bf16 values code * f. One lane per 16-value block: it reads the
@@ -230,6 +245,15 @@ extern "C" int l2c_nvfp4_tensor_scales(float *tensor_scales, float *alpha, const
   L2C_LAUNCH_CHECK();
   hipLaunchKernelGGL(nvfp4_scales_kernel, dim3(1), dim3(kThreads), 0, stream, tensor_scales, alpha,
                      other_decode, static_cast<const float *>(partials), parts);
+  L2C_LAUNCH_CHECK();
+  return hipSuccess;
+}
+
+extern "C" int l2c_nvfp4_tensor_scales_absmax(float *tensor_scales, float *alpha, const float *other_decode,
+                                              unsigned *absmax_bits, hipStream_t stream) {
+  if (!tensor_scales || !absmax_bits || (alpha && !other_decode)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(nvfp4_scales_absmax_kernel, dim3(1), dim3(1), 0, stream, tensor_scales, alpha, other_decode,
+                     absmax_bits);
   L2C_LAUNCH_CHECK();
   return hipSuccess;
 }

@@ -353,9 +353,15 @@ class ClassifierExperiment final : public appproto::Application {
     APP_HIP(hipMemcpyAsync(tokens_.get(), prompts_.get(), token_bytes, hipMemcpyDeviceToDevice, stream));
     const int B = static_cast<int>(d_.batch), W = static_cast<int>(d_.width), V = static_cast<int>(d_.vocab),
               S = static_cast<int>(d_.steps);
+    unsigned *absmax = format_->activation_absmax();
     for (int s = 0; s < S; ++s) {
-      APP_L2C(l2c_decoder_rmsnorm(normalized(s), tokens_.get(), embedding_.get(), norm_weight_.get(), W, V, B, stream));
-      classify(s, stream);
+      if (absmax)
+        APP_L2C(l2c_decoder_rmsnorm_absmax(normalized(s), tokens_.get(), embedding_.get(), norm_weight_.get(), W, V,
+                                           B, absmax, stream));
+      else
+        APP_L2C(l2c_decoder_rmsnorm(normalized(s), tokens_.get(), embedding_.get(), norm_weight_.get(), W, V, B,
+                                    stream));
+      classify(s, stream, absmax != nullptr);
       APP_L2C(l2c_decoder_softmax_argmax(probabilities_.get() + d_.row_at(0, s), logits(s), tokens_.get(),
                                          generated_.get(), V, B, S, s, stream));
     }
@@ -366,10 +372,15 @@ class ClassifierExperiment final : public appproto::Application {
 
   // The case's classifier for one step: whatever normalized(step) holds is
   // converted (NVFP4: with that step's alpha) and contracted with the weights.
-  void classify(long long step, hipStream_t stream) {
+  // `after_rmsnorm`: the step's rmsnorm filled the format's activation maximum
+  // (activation_absmax), so the encoding takes it instead of its own pass.
+  void classify(long long step, hipStream_t stream, bool after_rmsnorm) {
     DeviceTensor &x = step_inputs_[static_cast<size_t>(step)];
     float *alpha = alpha_ ? alpha_.get() + step : nullptr;
-    format_->encode(normalized(step), x, alpha, format_->decode_scale(weights_), stream);
+    if (after_rmsnorm)
+      format_->encode_activations(normalized(step), x, alpha, format_->decode_scale(weights_), stream);
+    else
+      format_->encode(normalized(step), x, alpha, format_->decode_scale(weights_), stream);
     format_->contract(logits(step), normalized(step), x, classifier_.get(), weights_, alpha,
                       static_cast<int>(d_.batch), static_cast<int>(d_.width), static_cast<int>(d_.vocab), stream);
   }
@@ -911,7 +922,7 @@ class Assessment {
       rmsnorm_float(model.embedding_row(model.prompt(b), &scratch), d.width, &x[static_cast<size_t>(b * d.width)]);
     });
     APP_HIP(hipMemcpyAsync(app.normalized(0), x.data(), x.size() * 4, hipMemcpyHostToDevice, stream));
-    app.classify(0, stream);
+    app.classify(0, stream, false);  // normalized(0) comes from the host here
     std::vector<float> device(static_cast<size_t>(d.batch * d.vocab));
     APP_HIP(hipMemcpyAsync(device.data(), app.logits(0), device.size() * 4, hipMemcpyDeviceToHost, stream));
     APP_HIP(hipStreamSynchronize(stream));

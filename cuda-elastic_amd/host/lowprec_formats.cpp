@@ -101,10 +101,17 @@ class Mxfp6 final : public Format {
 // Planes: E2M1 codes (two per byte, row-major), UE4M3 scales [rows][width/16],
 // the exact bf16 value of every element (what the contraction multiplies),
 // and the tensor's FP32 encode and decode scales (s, d). Owns the partial
-// maxima workspace of the tensor-scale reduction.
+// maxima workspace of the tensor-scale reduction (weights), and the word the
+// step's rmsnorm raises to the activations' maximum (the scales kernel clears
+// it), so a step skips the separate maximum pass over its activations.
 class Nvfp4 final : public Format {
  public:
   enum Plane { kCodes = 0, kScales = 1, kExpanded = 2, kTensor = 3 };
+  // The maximum word is allocated and cleared here, at set-up, never while a
+  // step may be under stream capture.
+  Nvfp4() : absmax_(l2c_decoder::device_array<unsigned>(1)) {
+    APP_HIP(hipMemset(absmax_.get(), 0, sizeof(unsigned)));
+  }
   int id() const override { return kNvfp4; }
   std::vector<size_t> plane_sizes(long long rows, long long width) const override {
     const size_t n = static_cast<size_t>(rows * width);
@@ -115,6 +122,15 @@ class Nvfp4 final : public Format {
     float *tensor = reinterpret_cast<float *>(t.plane(kTensor));
     APP_L2C(l2c_nvfp4_tensor_scales(tensor, alpha, alpha ? partner_decode : nullptr, x, t.rows * t.width,
                                     partials_.get(), stream));
+    APP_L2C(l2c_quantize_nvfp4(t.plane(kCodes), t.plane(kScales), reinterpret_cast<uint16_t *>(t.plane(kExpanded)), x,
+                               tensor, static_cast<int>(t.rows), static_cast<int>(t.width), stream));
+  }
+  unsigned *activation_absmax() override { return absmax_.get(); }
+  void encode_activations(const float *x, DeviceTensor &t, float *alpha, const float *partner_decode,
+                          hipStream_t stream) override {
+    float *tensor = reinterpret_cast<float *>(t.plane(kTensor));
+    APP_L2C(l2c_nvfp4_tensor_scales_absmax(tensor, alpha, alpha ? partner_decode : nullptr, activation_absmax(),
+                                           stream));
     APP_L2C(l2c_quantize_nvfp4(t.plane(kCodes), t.plane(kScales), reinterpret_cast<uint16_t *>(t.plane(kExpanded)), x,
                                tensor, static_cast<int>(t.rows), static_cast<int>(t.width), stream));
   }
@@ -154,6 +170,7 @@ class Nvfp4 final : public Format {
 
  private:
   l2c_decoder::DeviceArray<float> partials_;
+  l2c_decoder::DeviceArray<unsigned> absmax_;
 };
 
 }  // namespace

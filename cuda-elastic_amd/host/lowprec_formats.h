@@ -44,6 +44,16 @@ class Format {
   // activations), also *alpha = d(x) * *partner_decode on the device.
   virtual void encode(const float *x, DeviceTensor &t, float *alpha, const float *partner_decode,
                       hipStream_t stream) = 0;
+  // A device word (zero between steps) that the step's rmsnorm fills with the
+  // maximum |x| of the activations it writes (l2c_decoder_rmsnorm_absmax), for
+  // a format whose encoding needs the tensor maximum (NVFP4); else null.
+  virtual unsigned *activation_absmax() { return nullptr; }
+  // encode() for a step's activations, after the rmsnorm that filled
+  // activation_absmax() when the format has one.
+  virtual void encode_activations(const float *x, DeviceTensor &t, float *alpha, const float *partner_decode,
+                                  hipStream_t stream) {
+    encode(x, t, alpha, partner_decode, stream);
+  }
   // Device address of a tensor's FP32 decode scale d (NVFP4), else null.
   virtual const float *decode_scale(const DeviceTensor &) const { return nullptr; }
   // logits[batch][vocab] = x . w^T over the encoded operands, times *alpha when

@@ -42,8 +42,9 @@ KERNEL_SYMBOLS = (
     "l2c_rmsnorm", "l2c_softmax", "l2c_matvec", "l2c_fused", "l2c_matmul", "l2c_matmul_q",
     "l2c_quantize_mxfp4", "l2c_quantize_fp8", "l2c_to_bf16", "l2c_launch_shape",
     "l2c_strerror", "l2c_version",
-    "l2c_decoder_init_model", "l2c_decoder_rmsnorm", "l2c_decoder_softmax_argmax",
-    "l2c_quantize_mxfp6", "l2c_nvfp4_tensor_scales", "l2c_quantize_nvfp4", "l2c_to_bf16_x4",
+    "l2c_decoder_init_model", "l2c_decoder_rmsnorm", "l2c_decoder_rmsnorm_absmax", "l2c_decoder_softmax_argmax",
+    "l2c_quantize_mxfp6", "l2c_nvfp4_tensor_scales", "l2c_nvfp4_tensor_scales_absmax", "l2c_quantize_nvfp4",
+    "l2c_to_bf16_x4",
     "l2c_matmul_bf16", "l2c_matmul_mxfp6", "l2c_mxfp6_bytes",
     "l2c_matmul_qs", "l2c_quantize_mxfp8", "l2c_mxfp8_workspace_bytes", "l2c_matmul_qs_static",
     "l2c_copy_to_host",
@@ -99,9 +100,11 @@ def load() -> ctypes.CDLL:
         "l2c_launch_shape": [i, i, i, i, i, ctypes.POINTER(i), ctypes.POINTER(i), ctypes.POINTER(i)],
         "l2c_decoder_init_model": [p, p, p, i, i, p],
         "l2c_decoder_rmsnorm": [p, p, p, p, i, i, i, p],
+        "l2c_decoder_rmsnorm_absmax": [p, p, p, p, i, i, i, p, p],
         "l2c_decoder_softmax_argmax": [p, p, p, p, i, i, i, i, p],
         "l2c_quantize_mxfp6": [p, p, p, i, i, p],
         "l2c_nvfp4_tensor_scales": [p, p, p, p, ctypes.c_longlong, p, p],
+        "l2c_nvfp4_tensor_scales_absmax": [p, p, p, p, p],
         "l2c_quantize_nvfp4": [p, p, p, p, p, i, i, p],
         "l2c_to_bf16_x4": [p, p, ctypes.c_longlong, p],
         "l2c_matmul_bf16": [p, p, p, p, i, i, i, p],
@@ -273,6 +276,12 @@ def decoder_rmsnorm(normalized, tokens, embedding, weight, width, vocab, batch, 
     _check(load().l2c_decoder_rmsnorm(_vp(_ptr(normalized)), _vp(_ptr(tokens)), _vp(_ptr(embedding)),
                                       _vp(_ptr(weight)), width, vocab, batch, _vp(_stream(stream))),
            "l2c_decoder_rmsnorm")
+
+
+def decoder_rmsnorm_absmax(normalized, tokens, embedding, weight, width, vocab, batch, absmax_bits, stream=None):
+    _check(load().l2c_decoder_rmsnorm_absmax(_vp(_ptr(normalized)), _vp(_ptr(tokens)), _vp(_ptr(embedding)),
+                                             _vp(_ptr(weight)), width, vocab, batch, _vp(_ptr(absmax_bits)),
+                                             _vp(_stream(stream))), "l2c_decoder_rmsnorm_absmax")
 
 
 def decoder_softmax_argmax(probabilities, logits, tokens, generated, vocab, batch, steps, step,
@@ -456,6 +465,12 @@ def nvfp4_tensor_scales(tensor_scales, x, n, partials, alpha=None, other_decode=
     _check(load().l2c_nvfp4_tensor_scales(_vp(_ptr(tensor_scales)), _vp(_ptr(alpha)), _vp(_ptr(other_decode)),
                                           _vp(_ptr(x)), n, _vp(_ptr(partials)), _vp(_stream(stream))),
            "l2c_nvfp4_tensor_scales")
+
+
+def nvfp4_tensor_scales_absmax(tensor_scales, absmax_bits, alpha=None, other_decode=None, stream=None):
+    _check(load().l2c_nvfp4_tensor_scales_absmax(_vp(_ptr(tensor_scales)), _vp(_ptr(alpha)),
+                                                 _vp(_ptr(other_decode)), _vp(_ptr(absmax_bits)),
+                                                 _vp(_stream(stream))), "l2c_nvfp4_tensor_scales_absmax")
 
 
 def quantize_nvfp4(codes, scales, x, tensor_scales, rows, width, expanded=None, stream=None):

@@ -202,6 +202,11 @@ int l2c_to_bf16(uint16_t *out, const float *in, size_t n, hipStream_t stream);
  *   maximum is 0), tensor_scales[1] = d = 1 / s, and, when alpha is not NULL,
  *   *alpha = d * *other_decode, all FP32 on the device. partials: a device
  *   workspace of L2C_NVFP4_PARTIALS floats. Two launches, no atomics, no memset.
+ * l2c_nvfp4_tensor_scales_absmax: the same three values from a maximum that
+ *   l2c_decoder_rmsnorm_absmax left in *absmax_bits (the float's bits), which it
+ *   then sets to 0 for the next one: one single-lane launch. No counterpart in
+ *   the reference, whose tensor maximum is a separate pass over x; this pair
+ *   saves the lowprec NVFP4 step that pass.
  * l2c_quantize_nvfp4: x [rows][width] (width % 16 == 0) to E2M1 codes (two per
  *   byte, even index in the low nibble) and UE4M3 scales[rows][width / 16]:
  *   scale code UE4M3((block max / 6) * s), codes E2M1((v * s) / f), f the scale's
@@ -217,6 +222,8 @@ int l2c_quantize_mxfp6(uint8_t *codes, uint8_t *scales, const float *x, int rows
 int l2c_mxfp6_bytes(int rows, int width, size_t *code_bytes, size_t *scale_bytes);
 int l2c_nvfp4_tensor_scales(float *tensor_scales, float *alpha, const float *other_decode,
                             const float *x, long long n, float *partials, hipStream_t stream);
+int l2c_nvfp4_tensor_scales_absmax(float *tensor_scales, float *alpha, const float *other_decode,
+                                   unsigned *absmax_bits, hipStream_t stream);
 int l2c_quantize_nvfp4(uint8_t *codes, uint8_t *scales, uint16_t *expanded_bf16, const float *x,
                        const float *tensor_scales, int rows, int width, hipStream_t stream);
 int l2c_to_bf16_x4(uint16_t *out, const float *in, long long n, hipStream_t stream);
@@ -250,6 +257,11 @@ int l2c_matmul_mxfp6(float *out, const uint8_t *X, const uint8_t *Xscales, const
  * l2c_decoder_rmsnorm: normalized[b][j] = weight[j] * (scale_b * E[t_b][j]) with
  *   t_b = tokens[b], scale_b = 1 / sqrtf(sum_j E[t_b][j]^2 / width + 1e-5f); a token
  *   outside [0, vocab) gives a NaN row.
+ * l2c_decoder_rmsnorm_absmax: the same, and the maximum of |normalized| over
+ *   the batch (NaNs ignored) raised into *absmax_bits as a float's bits by
+ *   atomic maximum (exact in any order); the word must start at 0 (or at a
+ *   maximum to extend). No counterpart in the reference: it feeds
+ *   l2c_nvfp4_tensor_scales_absmax.
  * l2c_decoder_softmax_argmax: probabilities[b][r] = expf(logits[b][r] - max_b) / sum_b;
  *   t = index of the first maximum probability (-1 if none); tokens[b] = t and
  *   generated[b * steps + step] = t.
@@ -259,6 +271,9 @@ int l2c_decoder_init_model(float *embedding, float *classifier, float *norm_weig
                            int vocab, hipStream_t stream);
 int l2c_decoder_rmsnorm(float *normalized, const int *tokens, const float *embedding,
                         const float *weight, int width, int vocab, int batch, hipStream_t stream);
+int l2c_decoder_rmsnorm_absmax(float *normalized, const int *tokens, const float *embedding,
+                               const float *weight, int width, int vocab, int batch,
+                               unsigned *absmax_bits, hipStream_t stream);
 int l2c_decoder_softmax_argmax(float *probabilities, const float *logits, int *tokens,
                                int *generated, int vocab, int batch, int steps, int step,
                                hipStream_t stream);

@@ -216,3 +216,41 @@ def test_application_bench_and_in_process(torch_gpu, l2c):
     print("case decoder in-process check", flush=True)
     code, record, _ = l2c.decoder(sets(40, 96, 16, 5), in_process=True)
     assert code == 0 and record["status"] == "pass"
+
+
+@pytest.mark.parametrize("width,vocab,batch", [(16384, 50, 1024), (16384, 60, 601), (16384, 50, 65), (3000, 50, 64),
+                                               (1001, 40, 7), (20000, 30, 3)])
+def test_rmsnorm_absmax(torch_gpu, l2c, width, vocab, batch):
+    """l2c_decoder_rmsnorm_absmax writes what l2c_decoder_rmsnorm writes, bit for
+    bit, and raises the word to max |normalized| over the batch (NaN rows of
+    out-of-range tokens ignored). Shapes cover the two-row pipelined kernel
+    (16384 wide, batch >= 512, with a ragged last pair at 601), the
+    register-resident kernels (aligned and not: width 1001) and the streamed
+    one (20000).
+    A second call from a word already above the batch's maximum leaves it
+    there."""
+    torch = torch_gpu
+    print(f"case decoder_rmsnorm_absmax width={width} vocab={vocab} batch={batch}", flush=True)
+    rng = np.random.default_rng(width + batch)
+    e = (rng.standard_normal((vocab, width)) * 3.0).astype(np.float32)
+    w = rng.uniform(-1.5, 1.5, width).astype(np.float32)
+    tokens = rng.integers(0, vocab, batch).astype(np.int32)
+    tokens[::5] = vocab + 3  # out of range: NaN rows
+    tokens[1] = 0
+    td, ed, wd = dev(torch, tokens), dev(torch, e), dev(torch, w)
+    plain = torch.empty(batch * width, dtype=torch.float32, device="cuda")
+    fused = torch.full((batch * width,), 7.0, dtype=torch.float32, device="cuda")
+    word = torch.zeros(1, dtype=torch.int32, device="cuda")
+    l2c.decoder_rmsnorm(plain, td, ed, wd, width, vocab, batch)
+    l2c.decoder_rmsnorm_absmax(fused, td, ed, wd, width, vocab, batch, word)
+    torch.cuda.synchronize()
+    p, f = plain.cpu().numpy(), fused.cpu().numpy()
+    np.testing.assert_array_equal(p.view(np.uint32), f.view(np.uint32))
+    want = np.nanmax(np.abs(p))
+    got = word.cpu().numpy().view(np.float32)[0]
+    assert got == want, (got, want)
+    high = np.float32(want * 2)
+    word.copy_(torch.from_numpy(np.array([high], np.float32).view(np.int32)))
+    l2c.decoder_rmsnorm_absmax(fused, td, ed, wd, width, vocab, batch, word)
+    torch.cuda.synchronize()
+    assert word.cpu().numpy().view(np.float32)[0] == high

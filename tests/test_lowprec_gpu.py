@@ -210,3 +210,31 @@ def test_nvfp4_classifier_bound(torch_gpu, l2c):
     wc, wsc = oracle.quantize_nvfp4(cls, rows, cols, sw)
     check_bound(out.cpu().numpy(), lo.dequantize_nvfp4(xc, xsc, batch, cols),
                 lo.dequantize_nvfp4(wc, wsc, rows, cols), float(a), cols)
+
+
+@pytest.mark.parametrize("name,rows,width", [("crafted", 130, 256), ("random", 333, 2048), ("random", 3, 16)])
+def test_nvfp4_tensor_scales_from_absmax(torch_gpu, l2c, name, rows, width):
+    """The tensor scales from a maximum word (as l2c_decoder_rmsnorm_absmax
+    leaves it) equal those of the two-pass reduction over x bit for bit, alpha
+    included, and the word is cleared afterwards; a zero word gives s = d = 1."""
+    torch = torch_gpu
+    print(f"case nvfp4_tensor_scales_absmax {name} {rows}x{width}", flush=True)
+    x = inputs(name, rows, width)
+    f32 = torch.float32
+    xd = dev(torch, x)
+    other = torch.tensor([0.75], dtype=f32, device="cuda")
+    partials = torch.empty(l2c.NVFP4_PARTIALS, dtype=f32, device="cuda")
+    ts_a = torch.full((2,), np.nan, dtype=f32, device="cuda")
+    ts_b = torch.full((2,), np.nan, dtype=f32, device="cuda")
+    alpha_a = torch.full((1,), np.nan, dtype=f32, device="cuda")
+    alpha_b = torch.full((1,), np.nan, dtype=f32, device="cuda")
+    l2c.nvfp4_tensor_scales(ts_a, xd, rows * width, partials, alpha=alpha_a, other_decode=other)
+    word = torch.from_numpy(np.array([np.max(np.abs(x))], np.float32).view(np.int32)).cuda()
+    l2c.nvfp4_tensor_scales_absmax(ts_b, word, alpha=alpha_b, other_decode=other)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ts_a.cpu().numpy().view(np.uint32), ts_b.cpu().numpy().view(np.uint32))
+    np.testing.assert_array_equal(alpha_a.cpu().numpy().view(np.uint32), alpha_b.cpu().numpy().view(np.uint32))
+    assert word.cpu().numpy()[0] == 0
+    l2c.nvfp4_tensor_scales_absmax(ts_b, word)
+    torch.cuda.synchronize()
+    assert ts_b.cpu().numpy().tolist() == [1.0, 1.0]
