@@ -382,11 +382,12 @@ def decoder(args, in_process: bool = False, timeout=None):
     return proc.returncode, record, proc.stderr
 
 
-def lowprec(case, args, in_process: bool = False, timeout=None):
+def lowprec(case, args, in_process: bool = False, timeout=None, env=None):
     """Runs one case ("fp32", "bf16", "mxfp6", "nvfp4") of the lowprec
     classifier experiment; returns (exit_code, record dict or None, stdout +
     stderr text). args: the loom_private options, or ["--selftest"], or
-    ["--accuracy"]."""
+    ["--accuracy"]. env: extra environment variables for the child process
+    (e.g. {"L2C_LOWPREC_AMAX_IN_RMSNORM": "1"})."""
     import json
     args = [str(a) for a in args]
     index = LOWPREC_CASES.index(case)
@@ -401,7 +402,8 @@ def lowprec(case, args, in_process: bool = False, timeout=None):
     exe = os.path.join(LOWPREC_DIR, case)
     if not os.path.exists(exe):
         raise FileNotFoundError(f"{exe} is not built")
-    proc = subprocess.run([exe] + args, capture_output=True, text=True, timeout=timeout)
+    proc = subprocess.run([exe] + args, capture_output=True, text=True, timeout=timeout,
+                          env=dict(os.environ, **env) if env else None)
     record = None
     for line in proc.stdout.splitlines():
         if line.startswith("RESULT "):

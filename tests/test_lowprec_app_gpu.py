@@ -12,9 +12,9 @@ pytestmark = pytest.mark.gpu
 CASES = ["fp32", "bf16", "mxfp6", "nvfp4"]
 
 
-def run(l2c, case, args, timeout=300):
-    print(f"case lowprec {case} {' '.join(args)}", flush=True)
-    code, record, text = l2c.lowprec(case, args, timeout=timeout)
+def run(l2c, case, args, timeout=300, env=None):
+    print(f"case lowprec {case} {' '.join(args)}{' ' + str(env) if env else ''}", flush=True)
+    code, record, text = l2c.lowprec(case, args, timeout=timeout, env=env)
     print(text[-3000:], flush=True)
     return code, record, text
 
@@ -101,3 +101,18 @@ def test_accuracy_matches_published(torch_gpu, l2c, case):
         # order could move a near-tie; a token that differs then changes that
         # sequence's later steps.)
         assert d["tokens"]["agree"] == tokens, (i, d["tokens"])
+
+
+@pytest.mark.parametrize("args", [["--set", "fixture=1"], ["--preset", "large", "--action", "check", "--launch", "both"]])
+def test_nvfp4_amax_in_rmsnorm_changes_nothing(torch_gpu, l2c, args):
+    """With L2C_LOWPREC_AMAX_IN_RMSNORM=1 the NVFP4 steps take the activations'
+    maximum from the rmsnorm (l2c_decoder_rmsnorm_absmax and
+    l2c_nvfp4_tensor_scales_absmax) instead of a pass of their own: the check
+    passes and every output digest equals the default path's."""
+    digests = []
+    for env in (None, {"L2C_LOWPREC_AMAX_IN_RMSNORM": "1"}):
+        code, record, text = run(l2c, "nvfp4", args, timeout=600, env=env)
+        assert code == 0, text[-2000:]
+        assert record["status"] == "pass"
+        digests.append({c["digest"] for c in record["checks"]})
+    assert len(digests[0]) == 1 and digests[0] == digests[1]
