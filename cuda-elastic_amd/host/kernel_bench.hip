@@ -47,8 +47,8 @@
 // library's own contraction over every output, relative to the largest
 // output magnitude (both apply the bf16 op's alpha of 0.5).
 //
-// `stage_wstep`, `stage_wpair`, `stage_split64` and `stage_split128` are
-// staging-only copies of the block-scaled MXFP4 contraction's operand DMA
+// `stage_wstep`, `stage_wpair`, `stage_split64`, `stage_split128` and
+// `stage_fp8` are staging-only copies of the block-scaled contractions' operand DMA
 // (BATCH x SIZE E4M3 X codes, ROWS x SIZE E2M1 W codes; no matrix-core work,
 // no fragment reads, no scales): 512-lane workgroups on an XCD-ordered tile
 // map, LDS DMA of 16 bytes a lane issued three steps ahead of its wait, one
@@ -57,8 +57,10 @@
 // 128 bytes a row every other step; stage_split64 and stage_split128: 256 x
 // 256 tiles with k split over two workgroups, interleaved 64-k halves of every
 // step (X 64 and W 32 bytes a row) or contiguous halves of k (X 128 and W 64
-// bytes a row, three stages). They time how the L2 serves each pattern of row
-// segments; `bytes` is the bytes staged.
+// bytes a row, three stages); stage_fp8: the fp8-weight kernel's 256 x 128
+// tiles, per step X 128 bytes a row and 128 rows of E4M3 W 128 bytes a row,
+// three stages. They time how the L2 serves each pattern of row segments;
+// `bytes` is the bytes staged.
 //
 //   l2c_kernel_bench ceiling
 // measures the matrix-core rate the contractions can reach: register-only
@@ -129,32 +131,33 @@ __global__ void sweep_kernel(const float4 *src, size_t n4, float never, float *s
 // Fills n floats with a deterministic pattern in [-1, 1) scaled by `scale`.
 // Staging-only copy of the block-scaled contraction's operand DMA: per step
 // an X tile (XR rows x XB bytes, step stride XS) and every WEVERY steps a W
-// tile (256 rows x WB bytes, stride WS) into LDS rings (STAGES X slots, WSLOTS
+// tile (WR rows x WB bytes of K / WDIV-byte rows, stride WS) into LDS rings (STAGES X slots, WSLOTS
 // W slots), issued STAGES - 1 steps ahead and waited for one step ahead. With
 // SPLIT == 2 the workgroups 2 T, 2 T + 1 (after the XCD remap) take halves of
 // tile T's k range: interleaved halves of every step or contiguous halves.
 typedef __attribute__((address_space(3))) void stage_lds_ptr;
-template <int XR, int XB, int XS, int WB, int WS, int WEVERY, int STAGES, int WSLOTS, int SPLIT, bool INTERLEAVE>
+template <int XR, int XB, int XS, int WB, int WS, int WEVERY, int STAGES, int WSLOTS, int SPLIT, bool INTERLEAVE,
+          int WR = 256, int WDIV = 2>
 __device__ __forceinline__ void stage_body(const uint8_t *X, const uint8_t *W, int M, int N, int K, float *sink) {
-  constexpr int kX = XR * XB, kW = 256 * WB;
+  constexpr int kX = XR * XB, kW = WR * WB;
   constexpr int kXI = kX / 8192, kWI = kW / 8192;  // DMA instructions per wave
   constexpr int kOut = (STAGES - 2) * kXI + kWI * (WEVERY == 1 ? STAGES - 2 : 1);
   static_assert(kOut == 6 || kOut == 8, "wait counts");
   __shared__ __attribute__((aligned(1024))) unsigned char lds[STAGES * kX + WSLOTS * kW];
-  const int wrowbytes = K / 2;  // E2M1 rows
+  const int wrowbytes = K / WDIV;  // E2M1 (2) or E4M3 (1) rows
   int v = blockIdx.x;
   const int total = gridDim.x;
   if (total % 8 == 0) v = (v % 8) * (total / 8) + v / 8;
   const int tile = v / SPLIT, kh = v % SPLIT;
   const int mtiles = M / XR;
-  const int m0 = (tile % mtiles) * XR, n0 = (tile / mtiles) * 256;
+  const int m0 = (tile % mtiles) * XR, n0 = (tile / mtiles) * WR;
   const int steps = K / 128 / (INTERLEAVE ? 1 : SPLIT);
   const int xk0 = INTERLEAVE ? kh * XB : kh * (K / SPLIT);
   const int wk0 = INTERLEAVE ? kh * WB : kh * (wrowbytes / SPLIT);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
   const __amdgpu_buffer_rsrc_t rx = l2c::buffer_rsrc(X + static_cast<size_t>(m0) * K, static_cast<uint32_t>(XR) * K);
   const __amdgpu_buffer_rsrc_t rw =
-      l2c::buffer_rsrc(W + static_cast<size_t>(n0) * wrowbytes, 256u * static_cast<uint32_t>(wrowbytes));
+      l2c::buffer_rsrc(W + static_cast<size_t>(n0) * wrowbytes, static_cast<uint32_t>(WR) * wrowbytes);
   constexpr int xl = XB / 16, wl = WB / 16;  // lanes per row
   int xsrc[kXI], wsrc[kWI];
 #pragma unroll
@@ -197,6 +200,7 @@ L2C_STAGE_KERNEL(stage_wstep_kernel, 128, 128, 128, 64, 64, 1, 4, 4, 1, false)
 L2C_STAGE_KERNEL(stage_wpair_kernel, 128, 128, 128, 128, 128, 2, 4, 2, 1, false)
 L2C_STAGE_KERNEL(stage_split64_kernel, 256, 64, 128, 32, 64, 1, 4, 4, 2, true)
 L2C_STAGE_KERNEL(stage_split128_kernel, 256, 128, 128, 64, 64, 1, 3, 3, 2, false)
+L2C_STAGE_KERNEL(stage_fp8_kernel, 256, 128, 128, 128, 128, 1, 3, 3, 1, false, 128, 1)
 
 __global__ void fill_kernel(float *p, size_t n, unsigned seed, float scale) {
   const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
@@ -573,7 +577,8 @@ int main(int argc, char **argv) {
   float *x = nullptr, *p = nullptr, *w = nullptr, *m = nullptr, *o1 = nullptr, *o2 = nullptr, *prod = nullptr;
   const bool needs_matrix = op != "rmsnorm" && op != "softmax" && op != "copy" && op != "rmsnorm_cold" &&
                             op != "softmax_cold" && op != "copy_cold" && op != "read";
-  const bool staging = op == "stage_wstep" || op == "stage_wpair" || op == "stage_split64" || op == "stage_split128";
+  const bool staging = op == "stage_wstep" || op == "stage_wpair" || op == "stage_split64" || op == "stage_split128" ||
+                       op == "stage_fp8";
   if (staging && (B % 256 != 0 || R % 256 != 0 || S % 512 != 0 || static_cast<long long>(256) * S > 0x7fffffffLL)) {
     std::fprintf(stderr, "staging ops need BATCH %% 256 == 0, ROWS %% 256 == 0, SIZE %% 512 == 0\n");
     return 2;
@@ -738,6 +743,8 @@ int main(int argc, char **argv) {
       else if (op == "stage_wpair")
         hipLaunchKernelGGL(stage_wpair_kernel, dim3(tiles128), dim3(512), 0,
                            s, X8, W8, B, R, S, read_sink);
+      else if (op == "stage_fp8")
+        hipLaunchKernelGGL(stage_fp8_kernel, dim3((B / 256) * (R / 128)), dim3(512), 0, s, X8, W8, B, R, S, read_sink);
       else if (op == "stage_split64")
         hipLaunchKernelGGL(stage_split64_kernel, dim3(2 * tiles256), dim3(512), 0,
                            s, X8, W8, B, R, S, read_sink);
@@ -747,7 +754,8 @@ int main(int argc, char **argv) {
       CHECK(hipGetLastError());
       // Every tile stages all of its X rows and W rows over the whole k range.
       bytes = op == "stage_wstep" || op == "stage_wpair" ? static_cast<double>(tiles128) * (128.0 * S + 256.0 * S / 2)
-                                                         : static_cast<double>(tiles256) * (256.0 * S + 256.0 * S / 2);
+              : op == "stage_fp8" ? static_cast<double>((B / 256) * (R / 128)) * (256.0 * S + 128.0 * S)
+                                  : static_cast<double>(tiles256) * (256.0 * S + 256.0 * S / 2);
     } else if (op == "read") {
       hipLaunchKernelGGL(sweep_kernel, dim3(4096), dim3(256), 0, s, reinterpret_cast<const float4 *>(x), vec / 4,
                          1.0e30f, read_sink);
