@@ -62,6 +62,12 @@
 // three stages. They time how the L2 serves each pattern of row segments;
 // `bytes` is the bytes staged.
 //
+// `mfma_f8f4`, `mfma_f8f8` and `mfma_bf16` run the random-operand loop of
+// `ceiling` below (E4M3 x E2M1, E4M3 x E4M3 scaled, bf16) as an op, with as
+// many loop trips as the shape's 2 BATCH SIZE ROWS FLOPs need: the matrix
+// cores' half of a contraction alone, beside the `stage_*` copies of its
+// staging half (and, under `python -m l2c.power`, its power).
+//
 //   l2c_kernel_bench ceiling
 // measures the matrix-core rate the contractions can reach: register-only
 // loops (no memory traffic) of v_mfma_f32_32x32x2_f32, v_mfma_f32_16x16x4_f32, v_mfma_f32_32x32x16_bf16
@@ -462,6 +468,21 @@ static void ceiling_line(const char *name, float *out, int blocks, int trips) {
               r1);
 }
 
+// The random-operand loop of one MFMA type as an op: one 512-lane block per
+// CU, `trips` loop trips; returns the loop's FLOPs.
+static double launch_mfma_loop(const std::string &op, float *out, int blocks, int trips, hipStream_t s) {
+  double mnk = 32.0 * 32 * 64;
+  if (op == "mfma_f8f4") {
+    hipLaunchKernelGGL((ceiling_kernel<kCeilF8F4, 1>), dim3(blocks), dim3(512), 0, s, out, trips);
+  } else if (op == "mfma_f8f8") {
+    hipLaunchKernelGGL((ceiling_kernel<kCeilF8F8, 1>), dim3(blocks), dim3(512), 0, s, out, trips);
+  } else {
+    hipLaunchKernelGGL((ceiling_kernel<kCeilBf16, 1>), dim3(blocks), dim3(512), 0, s, out, trips);
+    mnk = 32.0 * 32 * 16;
+  }
+  return 2.0 * mnk * 32.0 * trips * blocks * 8.0;  // 32 MFMAs a trip, 8 waves a block
+}
+
 static int run_ceilings() {
   int cus = 0;
   CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
@@ -575,8 +596,9 @@ int main(int argc, char **argv) {
   }
   const size_t vec = static_cast<size_t>(B) * S, mat = static_cast<size_t>(R) * S;
   float *x = nullptr, *p = nullptr, *w = nullptr, *m = nullptr, *o1 = nullptr, *o2 = nullptr, *prod = nullptr;
+  const bool mfma_loop = op == "mfma_f8f4" || op == "mfma_f8f8" || op == "mfma_bf16";
   const bool needs_matrix = op != "rmsnorm" && op != "softmax" && op != "copy" && op != "rmsnorm_cold" &&
-                            op != "softmax_cold" && op != "copy_cold" && op != "read";
+                            op != "softmax_cold" && op != "copy_cold" && op != "read" && !mfma_loop;
   const bool staging = op == "stage_wstep" || op == "stage_wpair" || op == "stage_split64" || op == "stage_split128" ||
                        op == "stage_fp8";
   if (staging && (B % 256 != 0 || R % 256 != 0 || S % 512 != 0 || static_cast<long long>(256) * S > 0x7fffffffLL)) {
@@ -666,6 +688,15 @@ int main(int argc, char **argv) {
   CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
   float *read_sink = nullptr;
   if (op == "read" || staging) CHECK(hipMalloc(&read_sink, 4));
+  // mfma_*: the loop trips that do the shape's 2 BATCH SIZE ROWS FLOPs.
+  int cus = 0, trips = 0;
+  float *loop_out = nullptr;
+  if (mfma_loop) {
+    CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+    CHECK(hipMalloc(&loop_out, static_cast<size_t>(cus) * 512 * 4));
+    const double per_trip = 2.0 * (op == "mfma_bf16" ? 32.0 * 32 * 16 : 32.0 * 32 * 64) * 32.0 * cus * 8.0;
+    trips = std::max(1, static_cast<int>(2.0 * B * static_cast<double>(mat) / per_trip + 0.5));
+  }
   VendorGemm vg;
   if (vendor) {
     const bool bf = op == "vendor_bf16";
@@ -704,6 +735,9 @@ int main(int argc, char **argv) {
                         S, R, ws, ws_bytes, s));
       bytes = vec * 2.0 + (mx ? mat / 2.0 + mat / 32.0 : mat + R * 4.0) + static_cast<double>(B) * R * 4;
       flops = 2.0 * B * static_cast<double>(mat);
+    } else if (mfma_loop) {
+      flops = launch_mfma_loop(op, loop_out, cus, trips, s);
+      CHECK(hipGetLastError());
     } else if (op == "cvt_mxfp8") {
       L2C(l2c_quantize_mxfp8(ws, ws_bytes, xb, B, S, s));
       bytes = vec * (2.0 + 1.0 + 1.0 / 32);

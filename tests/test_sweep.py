@@ -164,3 +164,19 @@ def test_overlap_summary_on_a_synthetic_trace(tmp_path):
     assert s["product_us"] == 100.0 and s["gap_us"] == 30.0 and s["period_us"] == 130.0
     assert s["rows"]["rmsnorm"] == {"n": 4, "start_us": 5.0, "end_us": 45.0, "inside_product": 1.0}
     assert s["rows"]["softmax"] == {"n": 4, "start_us": -30.0, "end_us": -5.0, "inside_product": 0.0}
+
+
+def test_power_parsers():
+    """l2c.power reads amd-smi's socket power, rocm-smi's shader clock and the
+    kernel bench's result line as those tools print them on MI355X."""
+    from l2c import power
+    amd = "GPU: 0\n    POWER:\n        SOCKET_POWER: 1310 W\n        GFX_VOLTAGE: N/A\n"
+    assert power.parse_socket_power(amd) == 1310.0
+    assert power.parse_socket_power("GPU: 0\n    POWER:\n        SOCKET_POWER: N/A\n") is None
+    smi = "==== Current clock frequencies ====\nGPU[0]\t\t: sclk clock level: 1: (1963Mhz)\n"
+    assert power.parse_sclk(smi) == 1963.0
+    assert power.parse_sclk("GPU[0]\t\t: sclk clock level: S: (95Mhz)") == 95.0
+    line = ("op=fp8s batch=1024 size=16384 rows=8192 iters=30000 warmup=608 avg_us=126.760 "
+            "bytes=201359360 gbps=1588.5 tflops=2168.491")
+    rec = power.parse_result(line)
+    assert rec["op"] == "fp8s" and rec["avg_us"] == 126.76 and rec["iters"] == 30000.0

@@ -18,7 +18,8 @@ SHAPE = (256, 1024, 512)  # batch, size (k), rows: every op's divisibility holds
 OPS = ["rmsnorm", "softmax", "gemv", "naive", "fused", "matmul", "mxfp4", "fp8", "mxfp4s", "mxfp4s_narrow", "fp8s",
        "cvt_mxfp8", "bf16", "mxfp6", "cvt_bf16", "cvt_mxfp6", "cvt_nvfp4", "copy", "gemv_cold", "gemv_cold_copy",
        "read_cold", "rmsnorm_cold", "softmax_cold", "copy_cold", "read", "vendor_f32", "vendor_bf16",
-       "stage_wstep", "stage_wpair", "stage_split64", "stage_split128", "stage_fp8"]
+       "stage_wstep", "stage_wpair", "stage_split64", "stage_split128", "stage_fp8", "mfma_f8f4",
+       "mfma_f8f8", "mfma_bf16"]
 
 
 def run(*args, timeout=180):
