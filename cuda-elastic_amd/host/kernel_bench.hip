@@ -335,7 +335,10 @@ __device__ unsigned mix32(unsigned x) {
   return x ^ (x >> 16);
 }
 
-enum { kCeilF32 = 0, kCeilBf16 = 1, kCeilFp6 = 2, kCeilF8F4 = 3, kCeilF8F8 = 4, kCeilF32x16 = 5 };
+enum {
+  kCeilF32 = 0, kCeilBf16 = 1, kCeilFp6 = 2, kCeilF8F4 = 3, kCeilF8F8 = 4, kCeilF32x16 = 5,
+  kCeilBf16x16 = 6, kCeilF8F4x16 = 7, kCeilF8F8x16 = 8  // the 16 x 16 shapes of the same types
+};
 
 // Each lane holds four operand sets; MFMA (q, t) multiplies set q by set
 // (q + t) % 4 into accumulator t. RANDOM: operand bits from a hash (fp32 and
@@ -374,7 +377,7 @@ __global__ __launch_bounds__(512) void ceiling_kernel(float *out, int n) {
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int t = 0; t < 8; ++t) c[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q], b[(q + t) & 3], c[t], 0, 0, 0);
-  } else if constexpr (TYPE == kCeilBf16) {
+  } else if constexpr (TYPE == kCeilBf16 || TYPE == kCeilBf16x16) {
     u32x4 a[4], b[4];
     for (int q = 0; q < 4; ++q)
       for (int v = 0; v < 4; ++v) {
@@ -385,9 +388,17 @@ __global__ __launch_bounds__(512) void ceiling_kernel(float *out, int n) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-          c[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[q]),
-                                                         __builtin_bit_cast(bf16x8, b[(q + t) & 3]), c[t], 0, 0, 0);
+        for (int t = 0; t < 8; ++t) {
+          if constexpr (TYPE == kCeilBf16) {
+            c[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[q]),
+                                                           __builtin_bit_cast(bf16x8, b[(q + t) & 3]), c[t], 0, 0, 0);
+          } else {
+            f32x4 d = {c[t][0], c[t][1], c[t][2], c[t][3]};
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[q]),
+                                                        __builtin_bit_cast(bf16x8, b[(q + t) & 3]), d, 0, 0, 0);
+            c[t][0] = d[0], c[t][1] = d[1], c[t][2] = d[2], c[t][3] = d[3];
+          }
+        }
   } else if constexpr (TYPE == kCeilFp6) {
     i32x8 a[4], b[4];
     for (int q = 0; q < 4; ++q)
@@ -404,7 +415,8 @@ __global__ __launch_bounds__(512) void ceiling_kernel(float *out, int n) {
   } else {
     // A: 32 E4M3 codes a lane (1.0 = 0x38); B: 32 E2M1 codes in 4 VGPRs
     // (1.0 = 0x2) or 32 E4M3 codes.
-    constexpr bool kFp4 = TYPE == kCeilF8F4;
+    constexpr bool kFp4 = TYPE == kCeilF8F4 || TYPE == kCeilF8F4x16;
+    constexpr bool k16 = TYPE == kCeilF8F4x16 || TYPE == kCeilF8F8x16;
     constexpr int kFmtB = kFp4 ? 4 : 0;
     i32x8 a[4], b[4];
     for (int q = 0; q < 4; ++q)
@@ -418,8 +430,15 @@ __global__ __launch_bounds__(512) void ceiling_kernel(float *out, int n) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-          c[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[q], b[(q + t) & 3], c[t], 0, kFmtB, 0, 127, 0, 127);
+        for (int t = 0; t < 8; ++t) {
+          if constexpr (!k16) {
+            c[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[q], b[(q + t) & 3], c[t], 0, kFmtB, 0, 127, 0, 127);
+          } else {
+            f32x4 d = {c[t][0], c[t][1], c[t][2], c[t][3]};
+            d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[q], b[(q + t) & 3], d, 0, kFmtB, 0, 127, 0, 127);
+            c[t][0] = d[0], c[t][1] = d[1], c[t][2] = d[2], c[t][3] = d[3];
+          }
+        }
   }
   float sum = 0.0f;
   for (int t = 0; t < 8; ++t)
@@ -447,10 +466,12 @@ static double ceiling_rate(float *out, int blocks, int n, int threads) {
   CHECK(hipEventElapsedTime(&ms, a, b));
   CHECK(hipEventDestroy(a));
   CHECK(hipEventDestroy(b));
-  const double mnk = TYPE == kCeilF32     ? 32.0 * 32 * 2
-                     : TYPE == kCeilF32x16 ? 16.0 * 16 * 4
-                     : TYPE == kCeilBf16   ? 32.0 * 32 * 16
-                                           : 32.0 * 32 * 64;  // scaled: k = 64
+  const double mnk = TYPE == kCeilF32                                 ? 32.0 * 32 * 2
+                     : TYPE == kCeilF32x16                             ? 16.0 * 16 * 4
+                     : TYPE == kCeilBf16                               ? 32.0 * 32 * 16
+                     : TYPE == kCeilBf16x16                            ? 16.0 * 16 * 32
+                     : TYPE == kCeilF8F4x16 || TYPE == kCeilF8F8x16 ? 16.0 * 16 * 128
+                                                                       : 32.0 * 32 * 64;  // scaled: k = 64
   const double waves = threads / 64.0;
   const double flops = 2.0 * mnk * 32.0 * n * reps * blocks * waves;  // 32 MFMAs a loop trip
   return flops / (ms * 1e9);
@@ -495,6 +516,9 @@ static int run_ceilings() {
   ceiling_line<kCeilF8F4>("fp8 x fp4 (E4M3 x E2M1, scaled) 32x32x64", out, blocks, 1000);
   ceiling_line<kCeilF8F8>("fp8 x fp8 (E4M3 x E4M3, scaled) 32x32x64", out, blocks, 1000);
   ceiling_line<kCeilF32x16>("fp32 16x16x4", out, blocks, 800);
+  ceiling_line<kCeilBf16x16>("bf16 16x16x32", out, blocks, 4000);
+  ceiling_line<kCeilF8F4x16>("fp8 x fp4 (E4M3 x E2M1, scaled) 16x16x128", out, blocks, 2000);
+  ceiling_line<kCeilF8F8x16>("fp8 x fp8 (E4M3 x E4M3, scaled) 16x16x128", out, blocks, 2000);
   CHECK(hipFree(out));
   return 0;
 }
