@@ -58,7 +58,7 @@ def test_mfma_ceilings(torch_gpu):
     r = run("ceiling", timeout=300)
     assert r.returncode == 0, r.stderr
     lines = [ln for ln in r.stdout.splitlines() if ln.startswith("ceiling mfma=")]
-    assert len(lines) == 6, r.stdout
+    assert len(lines) == 9, r.stdout  # six 32 x 32 (and fp32 16 x 16) loops, three 16 x 16 ones
     for ln in lines:
         rates = {k: float(v) for k, v in re.findall(r"(\w+_tflops)=([0-9.]+)", ln)}
         assert set(rates) == {"constant_tflops", "random_tflops", "random_one_wave_tflops"}, ln
