@@ -32,6 +32,7 @@
 namespace {
 
 constexpr int kThreads = 256;
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 constexpr int kAmaxBlocks = 1024;  // partial maxima of the tensor-scale pass
 
 // One workgroup per output tile: k-step t (128 values) of the 32 rows of
@@ -170,21 +171,52 @@ __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(uint8_t *__res
   const float s = tensor_scales[0];
   const unsigned sc = l2c::nvfp4_scale_code(amax, s);
   const float f = l2c::ue4m3_value(sc);
-  unsigned c[16];
+  // E2M1((v s) / f), the two steps in this order, by the hardware conversion
+  // at scale 1 (nearest-even, saturating at 6): it gives e2m1_code's code for
+  // every value but the negative ones that round to zero, where it keeps the
+  // sign; those become +0 below. Two codes a conversion, packed into byte k
+  // of the word (element 2k in the low nibble). A zero scale code zeroes the
+  // block (f is 0 there, so the quotients are not finite).
+  float r[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) c[i] = sc != 0 ? l2c::nvfp4_code(e[i], s, f) : 0u;
-  unsigned lo = 0, hi = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    lo |= c[i] << (4 * i);
-    hi |= c[8 + i] << (4 * i);
+  for (int i = 0; i < 16; ++i) {
+    const float t = e[i] * s;
+    r[i] = t / f;
   }
+  unsigned lo = 0, hi = 0;
+  lo = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(lo, r[0], r[1], 1.0f, 0);
+  lo = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(lo, r[2], r[3], 1.0f, 1);
+  lo = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(lo, r[4], r[5], 1.0f, 2);
+  lo = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(lo, r[6], r[7], 1.0f, 3);
+  hi = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(hi, r[8], r[9], 1.0f, 0);
+  hi = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(hi, r[10], r[11], 1.0f, 1);
+  hi = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(hi, r[12], r[13], 1.0f, 2);
+  hi = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(hi, r[14], r[15], 1.0f, 3);
+  auto positive_zeros = [](unsigned w) {
+    const unsigned nonzero = ((w & 0x77777777u) + 0x77777777u) & 0x88888888u;  // 8 where magnitude != 0
+    return w & (nonzero | 0x77777777u);
+  };
+  lo = sc != 0 ? positive_zeros(lo) : 0u;
+  hi = sc != 0 ? positive_zeros(hi) : 0u;
   reinterpret_cast<uint2 *>(codes)[blk] = make_uint2(lo, hi);
   scales[blk] = static_cast<uint8_t>(sc);
   if (expanded) {
+    // code * f, exact: an E2M1 value (at most 2 significant bits) times a
+    // UE4M3 value (at most 4) has at most 6, so its bf16 is its top half.
+    const f32x2 v[8] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(lo, 1.0f, 0),
+                        __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(lo, 1.0f, 1),
+                        __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(lo, 1.0f, 2),
+                        __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(lo, 1.0f, 3),
+                        __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(hi, 1.0f, 0),
+                        __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(hi, 1.0f, 1),
+                        __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(hi, 1.0f, 2),
+                        __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(hi, 1.0f, 3)};
     unsigned b[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) b[i] = __float_as_uint(l2c::e2m1_value(c[i]) * f) >> 16;  // exact
+    for (int k = 0; k < 8; ++k) {
+      b[2 * k] = __float_as_uint(v[k][0] * f) >> 16;
+      b[2 * k + 1] = __float_as_uint(v[k][1] * f) >> 16;
+    }
     uint4 *dst = reinterpret_cast<uint4 *>(expanded) + blk * 2;
     dst[0] = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
     dst[1] = make_uint4(b[8] | (b[9] << 16), b[10] | (b[11] << 16), b[12] | (b[13] << 16), b[14] | (b[15] << 16));

@@ -238,3 +238,48 @@ def test_nvfp4_tensor_scales_from_absmax(torch_gpu, l2c, name, rows, width):
     l2c.nvfp4_tensor_scales_absmax(ts_b, word)
     torch.cuda.synchronize()
     assert ts_b.cpu().numpy().tolist() == [1.0, 1.0]
+
+
+def test_quantize_nvfp4_rounds_every_value_like_the_oracle(torch_gpu, l2c):
+    """The NVFP4 quantizer's E2M1 rounding (the hardware conversion, with its
+    negative zeros made +0) against the oracle's nearest-even search: blocks
+    [6, x1 .. x15] with tensor scale 1 have block scale 1, so each x's code is
+    E2M1(x) itself. The values: every float within 2^16 ulps of each rounding
+    threshold and of 6.0 (the top of the range, where codes saturate up to
+    6.375), every 16th float in [2^-3, 6.375), and a sample below 2^-3 down
+    to the subnormals, with both signs."""
+    torch = torch_gpu
+    print("case quantize_nvfp4 E2M1 rounding sweep", flush=True)
+    bits = []
+    for t in (0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 6.0):
+        b = int(np.float32(t).view(np.uint32))
+        bits.append(np.arange(b - 65536, b + 65536, dtype=np.uint32))
+    lo_b, hi_b = int(np.float32(0.125).view(np.uint32)), int(np.float32(6.375).view(np.uint32))
+    bits.append(np.arange(lo_b, hi_b, 16, dtype=np.uint32))
+    bits.append(np.arange(0, lo_b, 4099, dtype=np.uint32))
+    mag = np.unique(np.concatenate(bits)).view(np.float32)
+    mag = mag[mag < np.float32(6.375)]
+    vals = np.concatenate([mag, -mag])
+    per = 15
+    nblk = (vals.size + per - 1) // per
+    x = np.zeros((nblk, 16), dtype=np.float32)
+    x[:, 0] = 6.0
+    flat = np.zeros(nblk * per, dtype=np.float32)
+    flat[:vals.size] = vals
+    x[:, 1:] = flat.reshape(nblk, per)
+    rows, width = nblk, 16
+    f32 = torch.float32
+    ts = torch.tensor([1.0, 1.0], dtype=f32, device="cuda")
+    codes = torch.full((rows * width // 2,), 0xAB, dtype=torch.uint8, device="cuda")
+    scales = torch.full((rows * width // 16,), 0xAB, dtype=torch.uint8, device="cuda")
+    expanded = torch.full((rows * width,), -1, dtype=torch.int16, device="cuda")
+    l2c.quantize_nvfp4(codes, scales, dev(torch, x.reshape(-1)), ts, rows, width, expanded=expanded)
+    torch.cuda.synchronize()
+    assert np.all(scales.cpu().numpy() == 0x38)  # UE4M3 1.0: every block scale is 1
+    got = lo.unpack_e2m1(codes.cpu().numpy(), rows * width).reshape(rows, width)
+    want = oracle.e2m1_encode(x.reshape(-1).astype(np.float64)).reshape(rows, width)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, [(float(x[i, j]), int(got[i, j]), int(want[i, j])) for i, j in bad[:8]]
+    exp = lo.bf16_value(expanded.cpu().numpy().view(np.uint16)).reshape(rows, width)
+    values = np.array([oracle.lib().orc_e2m1_value(c) for c in range(16)], dtype=np.float64)
+    np.testing.assert_array_equal(exp, values[want].astype(exp.dtype))
